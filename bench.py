@@ -1,0 +1,327 @@
+#!/usr/bin/env python
+"""Benchmark of the paged-KV attention path on one MI355X.
+
+Headline (``value``): BASELINE config 4, paged decode at peak concurrency across a 28-layer stack. One step = the 28
+layers' ``Attention.forward`` decode calls (KV store of the new token + split-KV paged decode) for 150 sequences
+with contexts U[256, 2048], 16 query / 2 KV heads, head_dim 128, bf16, 256-token blocks; each layer has its own
+[2048, 256, 2, 128] K and V planes and its own q, seeded independently; the block tables (non-overlapping ids from a
+shuffled 2048-block pool) are shared by the layers, as an engine's are. The step is captured into a HIP graph and
+replayed, as the reference engine runs its decode step. ``value`` = algorithmic bytes of the step / step time.
+
+Beside it: the decode kernel's roofline (average launch duration from a graph of the 28 decode launches, HIP
+events on the launch stream), the prefill metric on BASELINE config 2 (varlen causal prefill, TFLOP/s against the
+bf16 dense MFMA peak, inputs rotated through > 256 MB so the Infinity Cache cannot serve them) plus a compute-bound
+supplementary prefill shape, and the CPU baseline: the oracle's torch path on the host cores over a bounded sample of
+the same decode workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--decode-only]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
+H, HK, D, BS = 16, 2, 128, 256
+SCALE = D ** -0.5
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
+    p.add_argument("--decode-only", action="store_true", help="headline decode only (no prefill legs)")
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget")
+    return p.parse_args()
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+
+def _graph_ms(fn, reps: int, warm: int = 3) -> float:
+    """Captures fn() in a HIP graph (after one eager warm-up call) and returns ms per replay over `reps` replays,
+    timed by HIP events on the current stream."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warm):
+        g.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        g.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / reps
+
+
+def decode_bytes(lens) -> int:
+    """Algorithmic HBM bytes of one decode launch: K+V of every context token, q and o, context_lens and the block
+    table entries read."""
+    toks = sum(lens)
+    blocks = sum((n + BS - 1) // BS for n in lens)
+    return toks * HK * D * 2 * 2 + len(lens) * H * D * 2 * 2 + 4 * (len(lens) + blocks)
+
+
+def store_bytes(n: int) -> int:
+    """Algorithmic bytes of storing n tokens' K/V rows: read k and v rows, write them, read the slots."""
+    return n * HK * D * 2 * 2 * 2 + 4 * n
+
+
+def prefill_units(nq, nk):
+    """(flops, bytes) of a varlen causal prefill: QK^T and PV over unmasked pairs; q, o and the K/V read once."""
+    pairs = sum(sum(k - q + i + 1 for i in range(q)) for q, k in zip(nq, nk))
+    flops = 4 * D * H * pairs
+    nbytes = sum(nq) * H * D * 2 * 2 + sum(nk) * HK * D * 2 * 2
+    return flops, nbytes
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+
+class DecodeWorkload:
+    """150 sequences x 28 layers, contexts U[256, 2048]."""
+
+    B, LAYERS, POOL = 150, 28, 2048
+
+    def __init__(self, dev):
+        import torch
+
+        from voxcpm2_arabic_dialects_turbo_amd import runner
+        from voxcpm2_arabic_dialects_turbo_amd.layers import Attention
+
+        gen = torch.Generator().manual_seed(100)
+        self.lens = torch.randint(256, 2049, (self.B,), generator=gen).tolist()
+        perm = torch.randperm(self.POOL, generator=gen).tolist()
+        tasks, at = [], 0
+        for n in self.lens:
+            nb = (n + BS - 1) // BS
+            tasks.append(runner.RunnerTask(perm[at:at + nb], n, n - 1, BS))
+            at += nb
+        self.tasks = tasks
+        self.layers = [Attention(H, D, SCALE, HK) for _ in range(self.LAYERS)]
+        self.kv = runner.allocate_kv_cache(self.layers, num_blocks=self.POOL, block_size=BS, device=dev)
+        self.qkv = torch.empty(self.LAYERS, self.B, (H + 2 * HK) * D, dtype=torch.bfloat16, device=dev)
+        for i in range(self.LAYERS):
+            g = torch.Generator(device=dev).manual_seed(100 + i)
+            self.kv[i].normal_(generator=g)
+            self.qkv[i].normal_(generator=g)
+        self.out = torch.empty(self.LAYERS, self.B, H * D, dtype=torch.bfloat16, device=dev)
+        runner.prepare_decode_context(tasks, BS, device=dev)
+        torch.cuda.synchronize()
+
+    def views(self, i):
+        q, k, v = self.qkv[i].split([H * D, HK * D, HK * D], dim=-1)
+        return q.view(self.B, H, D), k.view(self.B, HK, D), v.view(self.B, HK, D)
+
+    def step(self):
+        """One decode step: every layer's Attention.forward (store + decode). The outputs are left where the call
+        allocated them (the caller only views them: reference nanovllm_voxcpm/model/model.py:224-226)."""
+        outs = []
+        for i, layer in enumerate(self.layers):
+            q, k, v = self.views(i)
+            outs.append(layer(q, k, v))
+        return outs
+
+    def decode_launches(self):
+        """The step's 28 decode-kernel launches alone (no store), for the kernel's roofline."""
+        from voxcpm2_arabic_dialects_turbo_amd.context import get_context
+        from voxcpm2_arabic_dialects_turbo_amd.ops import decode_attention
+
+        ctx = get_context()
+        for i, layer in enumerate(self.layers):
+            q, _, _ = self.views(i)
+            decode_attention(q, layer.k_cache, layer.v_cache, ctx.context_lens, ctx.block_tables, SCALE,
+                             out=self.out[i].view(self.B, H, D))
+
+    def step_bytes(self) -> int:
+        return self.LAYERS * (decode_bytes(self.lens) + store_bytes(self.B))
+
+
+def bench_decode(args, dev):
+    import torch
+
+    w = DecodeWorkload(dev)
+    # full step in a graph (what `value` measures)
+    w.step()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        w.step()
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        g.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = start.elapsed_time(stop) / args.steps
+    # the decode kernel alone: graph of its 28 launches, HIP events on the launch stream
+    reps = max(10, args.steps // 2)
+    per_launch_ms = _graph_ms(w.decode_launches, reps) / w.LAYERS
+    res = dict(ms_per_step=ms_per_step, wall_s=wall, step_bytes=w.step_bytes(),
+               launch_bytes=decode_bytes(w.lens), launch_ms=per_launch_ms, lens=w.lens, workload=w)
+    return res
+
+
+def bench_prefill(dev):
+    """BASELINE config 2 prefill (packed causal varlen, production's no-prefix path) and a supplementary
+    compute-bound shape; per-launch ms from graphs of launches rotating over input sets."""
+    import torch
+
+    from voxcpm2_arabic_dialects_turbo_amd.ops import varlen_attention
+
+    out = {}
+    gen = torch.Generator().manual_seed(50)
+    lens = torch.randint(64, 513, (8,), generator=gen).tolist()
+    T = sum(lens)
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device=dev)
+    set_bytes = T * (H + 2 * HK) * D * 2
+    n_sets = max(2, (300 << 20) // set_bytes + 1)  # > 256 MB of inputs: not served from the Infinity Cache
+    qkv = torch.randn(n_sets, T, (H + 2 * HK) * D, generator=torch.Generator(device=dev).manual_seed(50),
+                      device=dev).to(torch.bfloat16)
+    o = torch.empty(T, H, D, dtype=torch.bfloat16, device=dev)
+
+    def run_c2():
+        for s in range(n_sets):
+            q, k, v = qkv[s].split([H * D, HK * D, HK * D], dim=-1)
+            varlen_attention(q.view(T, H, D), k.view(T, HK, D), v.view(T, HK, D), cu_seqlens_q=cu, cu_seqlens_k=cu,
+                             max_seqlen_q=max(lens), softmax_scale=SCALE, causal=True, out=o)
+
+    ms = _graph_ms(run_c2, 20) / n_sets
+    flops, nbytes = prefill_units(lens, lens)
+    tf = flops / (ms * 1e-3) / 1e12
+    bound = min(MFMA_BF16_PEAK_TFLOPS, flops / nbytes * HBM_PEAK_GBS / 1e3)
+    out["config2"] = dict(lens=lens, tokens=T, launch_us=round(ms * 1e3, 2), tflops=round(tf, 2),
+                          pct_mfma_peak=round(100 * tf / MFMA_BF16_PEAK_TFLOPS, 2),
+                          flop_per_byte=round(flops / nbytes, 1), roofline_bound_tflops=round(bound, 1),
+                          pct_of_roofline_bound=round(100 * tf / bound, 2), input_sets=n_sets)
+    del qkv
+    # supplementary compute-bound shape: 16 sequences x 2048 tokens, causal
+    L, NB = 2048, 16
+    T2 = L * NB
+    big = torch.randn(T2, (H + 2 * HK) * D, generator=torch.Generator(device=dev).manual_seed(51),
+                      device=dev).to(torch.bfloat16)
+    cu2 = torch.arange(0, T2 + 1, L, dtype=torch.int32, device=dev)
+    o2 = torch.empty(T2, H, D, dtype=torch.bfloat16, device=dev)
+    q, k, v = big.split([H * D, HK * D, HK * D], dim=-1)
+
+    def run_long():
+        varlen_attention(q.view(T2, H, D), k.view(T2, HK, D), v.view(T2, HK, D), cu_seqlens_q=cu2, cu_seqlens_k=cu2,
+                         max_seqlen_q=L, softmax_scale=SCALE, causal=True, out=o2)
+
+    ms2 = _graph_ms(run_long, 10)
+    flops2, _ = prefill_units([L] * NB, [L] * NB)
+    tf2 = flops2 / (ms2 * 1e-3) / 1e12
+    out["long_16x2048_supplementary"] = dict(launch_us=round(ms2 * 1e3, 1), tflops=round(tf2, 1),
+                                             pct_mfma_peak=round(100 * tf2 / MFMA_BF16_PEAK_TFLOPS, 2))
+    return out
+
+
+def cpu_baseline(w, budget_s: float):
+    """The oracle's torch path (fp32, as the reference's tests compute it) on the host cores over a bounded sample of
+    the same decode step: layer after layer (store + decode of 150 sequences) until the budget is spent."""
+    import torch
+
+    from oracle import attention as ref
+
+    threads = torch.get_num_threads()
+    lens = w.lens
+    tables = [t.block_table + [-1] * (8 - len(t.block_table)) for t in w.tasks]
+    slots = torch.tensor([ref.slot_of(t.block_table, t.seq_length - 1, BS) for t in w.tasks])
+    done, spent = 0, 0.0
+    while done < w.LAYERS and spent < budget_s:
+        kc, vc = w.layers[done].k_cache.cpu(), w.layers[done].v_cache.cpu()
+        q, k, v = (x.cpu() for x in w.views(done))
+        t0 = time.perf_counter()
+        ref.store_kvcache(k, v, kc, vc, slots)
+        ref.decode(q.float(), kc, vc, lens, tables, SCALE)
+        spent += time.perf_counter() - t0
+        done += 1
+    nbytes = done * (decode_bytes(lens) + store_bytes(len(lens)))
+    return dict(value=round(nbytes / spent / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+                sample=f"{done} of 28 layers of the config-4 decode step (store + decode, 150 sequences), "
+                       f"torch fp32 on CPU, {spent:.1f} s",
+                ms_per_step_extrapolated=round(spent / done * 28 * 1e3, 1))
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs on a single MI355X and has no multi-GPU path "
+              f"(--gpus {args.gpus} requested)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    from voxcpm2_arabic_dialects_turbo_amd import _lib
+
+    _lib.load()
+    res = bench_decode(args, dev)
+    value = res["step_bytes"] / (res["ms_per_step"] * 1e-3) / 1e9
+    achieved = res["launch_bytes"] / (res["launch_ms"] * 1e-3) / 1e9
+    line = {
+        "metric": "decode-attn HBM GB/s (%peak) @150 seqs; prefill attn TFLOP/s (%MFMA peak)",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "BASELINE config 4: paged decode, 150 seqs x 28 layers, ctx U[256,2048], 16 q / 2 kv heads, "
+                        "head_dim 128, bf16, 256-token blocks, 2048-block pool per layer; step = 28 "
+                        "Attention.forward decode calls (store + decode) replayed as one HIP graph",
+            "global_batch": DecodeWorkload.B,
+            "seq_len": "U[256,2048]",
+            "parallelism": "single GPU",
+            "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+            "step_bytes": res["step_bytes"],
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "decode_kernel<2>",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "launch_us": round(res["launch_ms"] * 1e3, 2),
+            "launch_bytes": res["launch_bytes"],
+        },
+    }
+    if not args.decode_only:
+        line["prefill"] = bench_prefill(dev)
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(res["workload"], args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

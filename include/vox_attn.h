@@ -1,0 +1,92 @@
+/* libvoxattn: MI355X (gfx950) paged-KV attention for the VoxCPM2 engine, C ABI.
+ *
+ * The three launch entry points replace the GPU calls that the reference's Attention.forward makes
+ * (reference: nanovllm_voxcpm/model/layers.py:326-362). All device buffers are owned by the caller; the library
+ * never allocates, frees or synchronizes, so every call is stream-ordered on `stream` (a hipStream_t, NULL = the
+ * null stream) and may be captured into a HIP graph. Element types: bf16 tensors are passed as raw pointers to
+ * 16-bit words, index tensors are int32. Strides are in elements.
+ *
+ * Every function returns VOX_OK or an error code; vox_last_error() returns the calling thread's message for the
+ * last failure. No function throws.
+ */
+#ifndef VOX_ATTN_H_
+#define VOX_ATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VOX_ABI_VERSION 1
+
+#define VOX_OK 0
+#define VOX_EINVAL 1 /* bad argument: shape, stride, alignment or null pointer (reference: the asserts of
+                        nanovllm_voxcpm/model/layers.py:299-302 and kernels/prefill_attn.py:107-108) */
+#define VOX_EHIP 2   /* the HIP runtime reported an error at launch */
+
+const char* vox_last_error(void);
+int vox_abi_version(void);
+
+/* KV slot scatter. Replaces store_kvcache / store_kvcache_kernel (reference: nanovllm_voxcpm/model/layers.py:266-305).
+ * For each token i < num_tokens with slot = slot_mapping[i] in [0, num_slots): copies the num_kv_heads*head_dim
+ * contiguous elements of key row i (rows key_row_stride apart) to k_cache + slot*num_kv_heads*head_dim, and
+ * likewise value -> v_cache. slot -1 (padding) is skipped, as in the reference; other out-of-range slots are skipped
+ * too instead of writing outside the cache. Bit-exact. */
+int vox_store_kvcache(const void* key, const void* value, int64_t key_row_stride, int64_t value_row_stride,
+                      void* k_cache, void* v_cache, int64_t num_slots, const int32_t* slot_mapping,
+                      int64_t num_tokens, int num_kv_heads, int head_dim, void* stream);
+
+/* Paged decode attention, one query token per sequence. Replaces the decode branch's
+ * flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache, cache_seqlens=context_lens, block_table=block_tables,
+ * softmax_scale, causal=True) (reference: nanovllm_voxcpm/model/layers.py:349-358).
+ *   q            bf16 [batch, num_heads, head_dim], sequence rows q_row_stride apart, heads head_dim apart
+ *   k/v_cache    bf16 [num_blocks, block_size, num_kv_heads, head_dim], contiguous
+ *   block_tables int32 [batch, bt_stride]; columns >= ceil(context_lens[b] / block_size) are never read
+ *   context_lens int32 [batch]; 0 = padded row, whose output is written as zeros
+ *   workspace    >= vox_decode_workspace_bytes(batch, max_blocks, block_size) bytes, contents scratch
+ *   counters     int32 [num_counters >= batch], all zero on entry; the call leaves them zero again. Calls that
+ *                share counters must be ordered on one stream.
+ *   out          bf16 [batch, num_heads, head_dim], contiguous
+ * Supported: head_dim 128, num_kv_heads 1 or 2, num_heads <= 16, block_size a multiple of 32. */
+int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
+                    int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
+                    int max_blocks, const int32_t* context_lens, int batch, int num_heads, int num_kv_heads,
+                    int head_dim, float softmax_scale, void* workspace, size_t workspace_bytes, int32_t* counters,
+                    int64_t num_counters, void* out, void* stream);
+
+/* Scratch bytes vox_decode_attn needs for a launch of this shape (split-KV partials). No reference counterpart:
+ * flash-attn sizes its split-KV buffers internally (reference call site: nanovllm_voxcpm/model/layers.py:350). */
+size_t vox_decode_workspace_bytes(int batch, int max_blocks, int block_size);
+
+/* Tokens per decode workgroup for this shape (a multiple of 128), and a process-wide override for tuning
+ * (0 restores the built-in choice). No reference counterpart. */
+int vox_decode_chunk_tokens(int batch, int max_blocks, int block_size);
+void vox_set_decode_chunk_tokens(int tokens);
+
+/* Varlen attention for prefill steps. Replaces flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q,
+ * max_seqlen_k, cu_seqlens_k, softmax_scale, causal=True, block_table) (reference: nanovllm_voxcpm/model/layers.py:
+ * 337-348), the Triton paged_prefill_attention / short_causal_attention in bf16 mode (reference:
+ * nanovllm_voxcpm/kernels/prefill_attn.py:98-124, kernels/short_attn.py:156-179), and, with causal = 0 and uniform
+ * lengths, flash_attn_func(q, k, v, softmax_scale, causal=False) (reference: nanovllm_voxcpm/model/layers.py:361).
+ *   q              bf16 [T, num_heads, head_dim], token rows q_row_stride apart
+ *   key/value      packed bf16 [Tk, num_kv_heads, head_dim] rows (used when block_tables is NULL)
+ *   k/v_cache      paged bf16 [num_blocks, block_size, num_kv_heads, head_dim] (used when block_tables != NULL)
+ *   cu_seqlens_q/k int32 [batch + 1]; both NULL selects uniform lengths uniform_seqlen_q / uniform_seqlen_k
+ *   causal         bottom-right aligned: query i of a sequence with nq queries and nk keys sees keys j <= nk-nq+i
+ *   out            bf16 [T, num_heads, head_dim], token rows out_row_stride apart
+ * Supported: head_dim 128, num_heads / num_kv_heads dividing 128. */
+int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const void* value,
+                     int64_t key_row_stride, int64_t value_row_stride, const void* k_cache, const void* v_cache,
+                     int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
+                     int max_blocks, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch,
+                     int max_seqlen_q, int uniform_seqlen_q, int uniform_seqlen_k, int num_heads, int num_kv_heads,
+                     int head_dim, float softmax_scale, int causal, void* out, int64_t out_row_stride,
+                     void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VOX_ATTN_H_ */

@@ -1,0 +1,134 @@
+"""The drop-in module on the GPU: Attention.forward driven by the runner's contexts through prefill and decode steps
+of a small engine loop, and the decode step captured into a HIP graph and replayed."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import attention as ref
+from tests._util import D, H, HK, attn_close, randn
+from voxcpm2_arabic_dialects_turbo_amd import runner
+from voxcpm2_arabic_dialects_turbo_amd.context import get_context, reset_context
+from voxcpm2_arabic_dialects_turbo_amd.layers import Attention
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+BS = 256
+SCALE = D ** -0.5
+
+
+@pytest.fixture(autouse=True)
+def _clean_context():
+    reset_context()
+    yield
+    reset_context()
+
+
+def _model(n_layers):
+    return torch.nn.ModuleList([Attention(H, D, SCALE, HK) for _ in range(n_layers)])
+
+
+def _step_qkv(gen, n):
+    qkv = randn(gen, n, (H + 2 * HK) * D).to(DEV)
+    q, k, v = qkv.split([H * D, HK * D, HK * D], dim=-1)
+    return q.view(n, H, D), k.view(n, HK, D), v.view(n, HK, D)
+
+
+def _expect(layer: Attention, q, tasks, new_tokens):
+    """Oracle: each sequence's query rows over its first seq_length cache slots (read back from the GPU cache)."""
+    kc, vc = layer.k_cache.cpu(), layer.v_cache.cpu()
+    outs, at = [], 0
+    for t, n in zip(tasks, new_tokens):
+        kb = ref.gather_pages(kc, t.block_table, t.seq_length).float()
+        vb = ref.gather_pages(vc, t.block_table, t.seq_length).float()
+        outs.append(ref.attend(q[at:at + n].float().cpu(), kb, vb, causal=True, scale=SCALE).view(n, H, D))
+        at += n
+    return torch.cat(outs)
+
+
+def test_engine_loop_prefill_with_prefix_then_decode_steps():
+    gen = torch.Generator().manual_seed(60)
+    model = _model(2)
+    runner.allocate_kv_cache(model, num_blocks=64, block_size=BS, device=DEV)
+    for m in model:  # a reference-prefix cache: the first blocks already hold keys
+        m.k_cache.copy_(randn(gen, *m.k_cache.shape).to(DEV))
+        m.v_cache.copy_(randn(gen, *m.v_cache.shape).to(DEV))
+    perm = torch.randperm(64, generator=gen).tolist()
+    lengths, cached = [40, 300, 513, 7], [0, 260, 100, 0]
+    tasks, at = [], 0
+    for n, c in zip(lengths, cached):
+        nb = (n + 4 + BS - 1) // BS  # room for the decode steps
+        tasks.append(runner.RunnerTask(perm[at:at + nb], n, c, BS))
+        at += nb
+    # prefill (a cached prefix -> keys through the block tables)
+    runner.prepare_prefill_context(tasks, BS, device=DEV)
+    assert get_context().block_tables is not None
+    new = [t.seq_length - t.num_cached_tokens for t in tasks]
+    for layer in model:
+        q, k, v = _step_qkv(gen, sum(new))
+        o = layer(q, k, v)
+        assert o.shape == (sum(new), H, D)
+        attn_close(o, _expect(layer, q, tasks, new), "prefill step")
+    # decode steps
+    for step in range(4):
+        for t in tasks:
+            t.seq_length += 1
+            t.num_cached_tokens = t.seq_length - 1
+        runner.prepare_decode_context(tasks, BS, device=DEV)
+        for layer in model:
+            q, k, v = _step_qkv(gen, len(tasks))
+            o = layer(q, k, v)
+            assert o.shape == (len(tasks), 1, H, D)
+            attn_close(o[:, 0], _expect(layer, q, tasks, [1] * len(tasks)), f"decode step {step}")
+
+
+def test_decode_step_captured_in_a_graph_replays_like_eager():
+    """Static buffers + torch.cuda.graph, as the reference's capture_cudagraph: warm-up eager call, capture, then
+    several replays with eager work and synchronizations between them, each checked against an eager run."""
+    gen = torch.Generator().manual_seed(61)
+    model = _model(3)
+    runner.allocate_kv_cache(model, num_blocks=64, block_size=BS, device=DEV)
+    for m in model:
+        m.k_cache.copy_(randn(gen, *m.k_cache.shape).to(DEV))
+        m.v_cache.copy_(randn(gen, *m.v_cache.shape).to(DEV))
+    max_bs, max_blocks = 16, 4
+    bufs = runner.DecodeGraphBuffers(max_bs, max_blocks, device=DEV)
+    q_in = torch.zeros(max_bs, (H + 2 * HK) * D, dtype=torch.bfloat16, device=DEV)
+    out = torch.zeros(3, max_bs, H * D, dtype=torch.bfloat16, device=DEV)
+
+    def forward(bs):
+        qkv = q_in[:bs]
+        q, k, v = qkv.split([H * D, HK * D, HK * D], dim=-1)
+        for i, layer in enumerate(model):
+            out[i, :bs] = layer(q.view(bs, H, D), k.view(bs, HK, D), v.view(bs, HK, D)).view(bs, -1)
+
+    bs = 16
+    bufs.bind(bs)
+    forward(bs)  # warm-up (context_lens all zero)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        forward(bs)
+    perm = torch.randperm(64, generator=gen).tolist()  # sequence i owns blocks perm[4i : 4i + 4]
+    for rep in range(4):
+        n = [16, 9, 16, 5][rep]
+        tasks = []
+        for i in range(n):
+            length = int(torch.randint(1, max_blocks * BS + 1, (1,), generator=gen))
+            nb = (length + BS - 1) // BS
+            tasks.append(runner.RunnerTask(perm[4 * i:4 * i + nb], length, length - 1, BS))
+        q_in[:n].copy_(randn(gen, n, (H + 2 * HK) * D).to(DEV))
+        runner.prepare_decode_context(tasks, BS, device=DEV)
+        bufs.load()
+        bufs.bind(bs)
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out[:, :n].clone()
+        runner.prepare_decode_context(tasks, BS, device=DEV)  # eager run of the same step
+        forward(n)
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, out[:, :n]), f"replay {rep} differs from eager"
+        for i, layer in enumerate(model):
+            q = q_in[:n, :H * D].view(n, H, D)
+            attn_close(out[i, :n].view(n, H, D), _expect(layer, q, tasks, [1] * n), f"replay {rep} layer {i}")

@@ -1,0 +1,116 @@
+"""The C ABI on the CPU: libvoxattn.so loads, exports every function include/vox_attn.h declares with the ABI
+version the bindings expect, and rejects bad arguments with VOX_EINVAL before touching the GPU (no launches)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from voxcpm2_arabic_dialects_turbo_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "vox_attn.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vox_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_bindings_agree():
+    assert _declared() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.vox_abi_version() == _lib.ABI_VERSION
+
+
+def test_only_one_hip_runtime_is_mapped():
+    """The library binds to the HIP runtime torch loaded (same SONAME), never a second copy."""
+    _lib.load()
+    maps = open("/proc/self/maps").read()
+    paths = {line.split()[-1] for line in maps.splitlines() if "libamdhip64" in line}
+    assert len(paths) <= 1, paths
+
+
+def _err():
+    return _lib.load().vox_last_error().decode()
+
+
+def test_store_rejects_bad_arguments_without_launching():
+    lib = _lib.load()
+    assert lib.vox_store_kvcache(None, None, 256, 256, None, None, 10, None, 0, 2, 128, None) == _lib.VOX_OK  # empty
+    assert lib.vox_store_kvcache(None, None, 256, 256, None, None, 10, None, 4, 2, 128, None) == _lib.VOX_EINVAL
+    assert "null pointer" in _err()
+    p = ctypes.c_void_p(16)  # never dereferenced: the checks fail first
+    assert lib.vox_store_kvcache(p, p, 100, 256, p, p, 10, p, 4, 2, 128, None) == _lib.VOX_EINVAL
+    assert "row stride" in _err()
+    assert lib.vox_store_kvcache(p, p, 256, 256, p, p, 0, p, 4, 2, 128, None) == _lib.VOX_EINVAL
+
+
+def _decode(**over):
+    p = ctypes.c_void_p(256)
+    a = dict(q=p, qs=16 * 128, kc=p, vc=p, nb=4, bs=256, bt=p, bts=8, mb=8, lens=p, b=2, h=16, hk=2, d=128,
+             scale=0.088, ws=p, wsb=1 << 30, cnt=p, ncnt=16, out=p, stream=None)
+    a.update(over)
+    return _lib.load().vox_decode_attn(*a.values())
+
+
+def test_decode_rejects_unsupported_shapes():
+    assert _decode(b=0) == _lib.VOX_OK
+    for over, msg in [(dict(d=64), "head_dim"), (dict(hk=4, h=16), "num_kv_heads"), (dict(h=32), "num_heads"),
+                      (dict(bs=100), "block_size"), (dict(bts=4), "block table"), (dict(ncnt=1), "counters"),
+                      (dict(wsb=10), "workspace"), (dict(qs=100), "row stride"), (dict(lens=None), "null"),
+                      (dict(scale=float("nan")), "finite")]:
+        assert _decode(**over) == _lib.VOX_EINVAL, over
+        assert msg in _err(), (over, _err())
+
+
+def test_decode_workspace_and_chunk_choice():
+    lib = _lib.load()
+    assert lib.vox_decode_workspace_bytes(0, 8, 256) == 0
+    for b, mb in [(1, 2), (40, 6), (150, 8), (512, 4)]:
+        chunk = lib.vox_decode_chunk_tokens(b, mb, 256)
+        assert chunk % 128 == 0 and 128 <= chunk <= 256
+        chunks = -(-mb * 256 // chunk)
+        assert lib.vox_decode_workspace_bytes(b, mb, 256) == b * chunks * (16 * 128 + 32) * 4
+    lib.vox_set_decode_chunk_tokens(512)
+    try:
+        assert lib.vox_decode_chunk_tokens(150, 8, 256) == 512
+    finally:
+        lib.vox_set_decode_chunk_tokens(0)
+    assert lib.vox_decode_chunk_tokens(150, 8, 256) == 128
+
+
+def test_prefill_rejects_bad_arguments():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    # valid apart from the fake pointers: never passed unmodified (it would launch)
+    args = [p, 2048, p, p, 256, 256, None, None, 0, 0, None, 0, 0, p, p, 2, 16, 0, 0, 16, 2, 128, 0.088, 1, p, 2048,
+            None]
+    bad = list(args)
+    bad[21] = 64  # head_dim
+    assert lib.vox_prefill_attn(*bad) == _lib.VOX_EINVAL and "head_dim" in _err()
+    bad = list(args)
+    bad[13] = None  # only one cu_seqlens
+    assert lib.vox_prefill_attn(*bad) == _lib.VOX_EINVAL and "cu_seqlens" in _err()
+    bad = list(args)
+    bad[19], bad[20] = 16, 3
+    assert lib.vox_prefill_attn(*bad) == _lib.VOX_EINVAL and "multiple" in _err()
+    bad = list(args)
+    bad[2] = None  # packed mode without key
+    assert lib.vox_prefill_attn(*bad) == _lib.VOX_EINVAL and "key/value" in _err()
+    zero = list(args)
+    zero[15] = 0  # empty batch: nothing to do
+    assert lib.vox_prefill_attn(*zero) == _lib.VOX_OK
+
+
+def test_python_errors_carry_the_library_message():
+    with pytest.raises(ValueError, match="head_dim"):
+        _lib.check(_decode(d=64), "decode_attn")

@@ -1,0 +1,135 @@
+"""GPU parity of the split-KV paged decode kernel (HIP kernel 3) against the oracle (fp32 on the same bf16 inputs):
+max-abs <= 2e-2 and mean-abs <= 2e-3."""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as ref
+from tests._util import BLOCK, D, H, HK, attn_close, paged_pool, randn, uniform_lens
+from tests.golden import make_golden
+from voxcpm2_arabic_dialects_turbo_amd import _lib
+from voxcpm2_arabic_dialects_turbo_amd.ops import decode_attention, flash_attn_with_kvcache
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+SCALE = D ** -0.5
+
+
+def _check(q, kc, vc, lens, tables, what, h=H, hk=HK):
+    out = decode_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), torch.tensor(lens, dtype=torch.int32, device=DEV),
+                           tables.to(DEV), SCALE)
+    torch.cuda.synchronize()
+    want = ref.decode(q.float().cpu(), kc, vc, lens, tables, SCALE)
+    return attn_close(out, want, what), out
+
+
+def test_decode_config1_golden():
+    """BASELINE config 1 (1 sequence, context 512, 4 shuffled blocks), inputs rounded to bf16 on the GPU."""
+    inp = make_golden.inputs("decode_c1")
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden.npz"), allow_pickle=False)
+    q, kc, vc = inp["q"].bfloat16(), inp["k_cache"].bfloat16(), inp["v_cache"].bfloat16()
+    _, out = _check(q, kc, vc, inp["lens"].tolist(), inp["tables"], "config 1")
+    attn_close(out, torch.from_numpy(g["decode_c1__out"]), "config 1 vs golden (fp32 inputs)")
+
+
+def test_decode_config3_shape():
+    """40 sequences, contexts U[200, 1500], 1024-block pool."""
+    gen = torch.Generator().manual_seed(30)
+    lens = uniform_lens(gen, 40, 200, 1500)
+    kc, vc, tables = paged_pool(gen, lens, 1024)
+    _check(randn(gen, 40, H, D), kc, vc, lens, tables, "config 3")
+
+
+def test_decode_ragged_contexts_and_stale_table_columns():
+    """Context lengths around every tile / chunk / block boundary; columns past a row's blocks hold garbage ids
+    (as captured graph buffers do) and must never be read."""
+    gen = torch.Generator().manual_seed(31)
+    lens = [1, 2, 31, 32, 33, 127, 128, 129, 255, 256, 257, 383, 511, 512, 513, 1000, 2047, 2048]
+    kc, vc, tables = paged_pool(gen, lens, 160, extra_cols=2)
+    tables[tables < 0] = 10 ** 9  # stale ids far outside the pool
+    tables[0, -1] = -7
+    _check(randn(gen, len(lens), H, D), kc, vc, lens, tables, "ragged")
+
+
+def test_decode_padded_rows_write_zeros():
+    gen = torch.Generator().manual_seed(32)
+    lens = [300, 0, 5, 0]
+    kc, vc, tables = paged_pool(gen, [300, 1, 5, 1], 8)
+    (_, _), out = _check(randn(gen, 4, H, D), kc, vc, lens, tables, "padded")
+    assert int(out[1].abs().sum()) == 0 and int(out[3].abs().sum()) == 0
+
+
+def test_decode_one_kv_head_tp2_shape():
+    """Tensor parallel 2 splits heads: 8 query heads over 1 KV head."""
+    gen = torch.Generator().manual_seed(33)
+    lens = uniform_lens(gen, 12, 1, 1200)
+    kc, vc, tables = paged_pool(gen, lens, 64, hk=1)
+    _check(randn(gen, 12, 8, D), kc, vc, lens, tables, "HK=1")
+
+
+def test_decode_strided_query_rows_and_small_blocks():
+    """q as a view of the qkv output (rows 2560 elements apart); 64-token blocks."""
+    gen = torch.Generator().manual_seed(34)
+    lens = uniform_lens(gen, 9, 1, 900)
+    kc, vc, tables = paged_pool(gen, lens, 200, block_size=64)
+    qkv = randn(gen, 9, (H + 2 * HK) * D)
+    q = qkv.to(DEV)[:, :H * D].view(9, H, D)
+    assert q.stride(0) == (H + 2 * HK) * D
+    out = decode_attention(q, kc.to(DEV), vc.to(DEV), torch.tensor(lens, dtype=torch.int32, device=DEV),
+                           tables.to(DEV), SCALE)
+    attn_close(out, ref.decode(q.float().cpu(), kc, vc, lens, tables, SCALE), "strided q")
+
+
+@pytest.mark.parametrize("chunk", [128, 256, 512, 2048])
+def test_decode_chunk_sizes_agree(chunk):
+    gen = torch.Generator().manual_seed(35)
+    lens = uniform_lens(gen, 20, 1, 2048)
+    kc, vc, tables = paged_pool(gen, lens, 200)
+    lib = _lib.load()
+    lib.vox_set_decode_chunk_tokens(chunk)
+    try:
+        _check(randn(gen, 20, H, D), kc, vc, lens, tables, f"chunk {chunk}")
+    finally:
+        lib.vox_set_decode_chunk_tokens(0)
+
+
+def test_decode_counters_are_left_zero_across_calls():
+    from voxcpm2_arabic_dialects_turbo_amd.ops import decode_counters
+
+    gen = torch.Generator().manual_seed(36)
+    for n in (30, 7, 30, 64):
+        lens = uniform_lens(gen, n, 100, 2048)
+        kc, vc, tables = paged_pool(gen, lens, 8 * n)
+        _check(randn(gen, n, H, D), kc, vc, lens, tables, f"batch {n}")
+        assert int(decode_counters(torch.device(DEV)).abs().sum()) == 0
+
+
+def test_decode_config4_layer_full_size():
+    """BASELINE config 4, one layer at full size: 150 sequences, contexts U[256, 2048], 2048-block pool."""
+    gen = torch.Generator().manual_seed(100)
+    lens = uniform_lens(gen, 150, 256, 2048)
+    kc, vc, tables = paged_pool(gen, lens, 2048)
+    _check(randn(gen, 150, H, D), kc, vc, lens, tables, "config 4 layer")
+
+
+def test_with_kvcache_entry_point_shapes():
+    """flash_attn_with_kvcache: [B, 1, H, D] decode and a [B, 3, H, D] multi-token query (bottom-right causal)."""
+    gen = torch.Generator().manual_seed(37)
+    lens = [40, 300, 257]
+    kc, vc, tables = paged_pool(gen, lens, 8)
+    q = randn(gen, 3, 1, H, D)
+    args = dict(cache_seqlens=torch.tensor(lens, dtype=torch.int32, device=DEV), block_table=tables.to(DEV),
+                softmax_scale=SCALE, causal=True)
+    out = flash_attn_with_kvcache(q.to(DEV), kc.to(DEV), vc.to(DEV), **args)
+    assert out.shape == (3, 1, H, D)
+    attn_close(out[:, 0], ref.decode(q[:, 0].float(), kc, vc, lens, tables, SCALE), "with_kvcache Lq=1")
+    q3 = randn(gen, 3, 3, H, D)
+    out3 = flash_attn_with_kvcache(q3.to(DEV), kc.to(DEV), vc.to(DEV), **args)
+    want = ref.varlen(q3.reshape(9, H, D).float(), [0, 3, 6, 9], [0, 40, 340, 597], k_cache=kc, v_cache=vc,
+                      block_tables=tables)
+    attn_close(out3.reshape(9, H, D), want, "with_kvcache Lq=3")

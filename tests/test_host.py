@@ -1,0 +1,237 @@
+"""Host logic on the CPU: the context builders against the oracle's per-token loops, HostPack, KV-cache
+allocation, decode graph buffers, and Attention.forward's dispatch (with the kernels recorded, not run)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import context as ctxref
+from voxcpm2_arabic_dialects_turbo_amd import layers, runner
+from voxcpm2_arabic_dialects_turbo_amd.context import get_context, reset_context, set_context
+from voxcpm2_arabic_dialects_turbo_amd.layers import Attention
+
+BS = 4  # small blocks: prefixes end inside blocks, sequences span several (as the reference's host tests do)
+
+
+@pytest.fixture(autouse=True)
+def _clean_context():
+    reset_context()
+    yield
+    reset_context()
+
+
+def _tasks(rng, n, warmup=False, block_size=BS):
+    tasks, next_block = [], 0
+    for i in range(n):
+        length = int(rng.integers(1, 15))
+        cached = 0 if warmup else int(rng.integers(0, length))
+        blocks = [] if warmup else list(range(next_block, next_block + (length + block_size - 1) // block_size))
+        next_block += len(blocks) + int(rng.integers(0, 3))
+        tasks.append(runner.RunnerTask(blocks, length, cached, block_size, seq_id=f"s{i}"))
+    return tasks
+
+
+def _snapshot():
+    c = get_context()
+    out = {"max": (c.is_prefill, c.max_seqlen_q, c.max_seqlen_k)}
+    for f in ("cu_seqlens_q", "cu_seqlens_k", "slot_mapping", "block_tables", "context_lens"):
+        v = getattr(c, f)
+        out[f] = None if v is None else (v.dtype, v.tolist())
+    return out
+
+
+@pytest.mark.parametrize("seed,warmup,graphs", [(0, False, False), (1, False, True), (2, True, False), (3, False, False),
+                                                (4, True, True)])
+def test_prefill_context_matches_the_per_token_loop(seed, warmup, graphs):
+    rng = np.random.default_rng(seed)
+    tasks = _tasks(rng, 9, warmup=warmup)
+    positions = runner.prepare_prefill_context(tasks, BS, device="cpu", graphs=graphs)
+    got = _snapshot()
+    pos, cu_q, cu_k, max_q, max_k, slots, tables = ctxref.prefill_context(BS, tasks, graphs=graphs)
+    assert (positions.dtype, positions.tolist()) == (torch.int64, pos)
+    assert got["cu_seqlens_q"] == (torch.int32, cu_q) and got["cu_seqlens_k"] == (torch.int32, cu_k)
+    assert got["max"] == (True, max_q, max_k)
+    assert got["slot_mapping"] == (torch.int32, slots)
+    assert got["block_tables"] == (None if tables is None else (torch.int32, tables))
+    assert got["context_lens"] is None
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_decode_context_matches_the_per_sequence_formulas(seed):
+    rng = np.random.default_rng(seed)
+    tasks = _tasks(rng, 11)
+    for t in tasks:  # decode: everything but the new token is cached
+        t.num_cached_tokens = t.seq_length - 1
+    positions = runner.prepare_decode_context(tasks, BS, device="cpu")
+    got = _snapshot()
+    pos, slots, lens, tables = ctxref.decode_context(BS, tasks)
+    assert (positions.dtype, positions.tolist()) == (torch.int64, pos)
+    assert got["slot_mapping"] == (torch.int32, slots)
+    assert got["context_lens"] == (torch.int32, lens)
+    assert got["block_tables"] == (torch.int32, tables)
+    assert got["max"] == (False, 0, 0)
+
+
+def test_host_pack_round_trips_dtypes_shapes_and_alignment():
+    pack = runner.HostPack("cpu")
+    a = np.arange(5, dtype=np.int64)
+    b = np.arange(7, dtype=np.int32).reshape(7)
+    c = np.arange(12, dtype=np.int32).reshape(3, 4) - 6
+    ia, ib, ic = pack.add(a), pack.add(b), pack.add(c)
+    views = pack.upload()
+    assert views[ia].dtype == torch.int64 and views[ia].tolist() == a.tolist()
+    assert views[ib].dtype == torch.int32 and views[ib].tolist() == b.tolist()
+    assert views[ic].shape == (3, 4) and views[ic].tolist() == c.tolist()
+    base = views[ia].data_ptr()  # parts start at 256-byte offsets of the one buffer
+    assert (views[ib].data_ptr() - base) % 256 == 0 and (views[ic].data_ptr() - base) % 256 == 0
+
+
+def test_allocate_kv_cache_assigns_layer_views():
+    model = torch.nn.ModuleList([Attention(16, 128, 128 ** -0.5, 2) for _ in range(3)]
+                                + [Attention(16, 128, 128 ** -0.5, 2, is_causal=False)])
+    kv = runner.allocate_kv_cache(model, num_blocks=5, block_size=256, device="cpu")
+    assert kv.shape == (3, 2, 5, 256, 2, 128) and kv.dtype == torch.bfloat16
+    for i, m in enumerate(runner.causal_attention_modules(model)):
+        assert m.k_cache.data_ptr() == kv[i, 0].data_ptr() and m.v_cache.data_ptr() == kv[i, 1].data_ptr()
+        assert m.k_cache.is_contiguous() and m.k_cache.stride(1) == 256
+    assert model[3].k_cache.numel() == 0  # non-causal layers get no cache
+    assert runner.kv_cache_block_bytes(runner.causal_attention_modules(model), 256) == 3 * 2 * 256 * 2 * 128 * 2
+    with pytest.raises(ValueError):
+        runner.allocate_kv_cache(model, num_blocks=5, block_size=128, device="cpu")
+
+
+def test_decode_graph_buffers_load_like_run_model():
+    bufs = runner.DecodeGraphBuffers(8, 4, device="cpu")
+    bufs.block_tables.fill_(77)  # stale columns from an earlier step stay
+    set_context(False, slot_mapping=torch.tensor([5, 9], dtype=torch.int32),
+                context_lens=torch.tensor([6, 10], dtype=torch.int32),
+                block_tables=torch.tensor([[1, 2], [3, 4]], dtype=torch.int32))
+    bufs.load()
+    assert bufs.slot_mapping.tolist() == [5, 9] + [-1] * 6
+    assert bufs.context_lens.tolist() == [6, 10] + [0] * 6
+    assert bufs.block_tables[:2].tolist() == [[1, 2, 77, 77], [3, 4, 77, 77]]
+    bufs.bind(4)
+    assert get_context().context_lens.shape == (4,) and not get_context().is_prefill
+    assert runner.graph_batch_sizes(40) == [1, 2, 4, 8, 16, 32, 40]
+
+
+# --- Attention.forward dispatch (kernels recorded) -------------------------------------------------------------------
+
+class _Recorder:
+    def __init__(self, monkeypatch):
+        self.calls = []
+        for name in ("store_kvcache", "flash_attn_varlen_func", "flash_attn_with_kvcache", "flash_attn_func"):
+            monkeypatch.setattr(layers, name, self._make(name))
+
+    def _make(self, name):
+        def fn(*args, **kwargs):
+            self.calls.append((name, args, kwargs))
+            return "o"
+        return fn
+
+
+def test_prefill_without_prefix_attends_over_the_step_kv(monkeypatch):
+    rec = _Recorder(monkeypatch)
+    attn = Attention(16, 128, 0.125, 2)
+    attn.k_cache, attn.v_cache = torch.zeros(2, 256, 2, 128), torch.zeros(2, 256, 2, 128)
+    q, k, v = torch.zeros(5, 16, 128), torch.zeros(5, 2, 128), torch.zeros(5, 2, 128)
+    cu = torch.tensor([0, 5], dtype=torch.int32)
+    slots = torch.arange(5, dtype=torch.int32)
+    set_context(True, cu, cu, 5, 5, slots, None, None)
+    assert attn(q, k, v) == "o"
+    (n0, a0, _), (n1, a1, kw1) = rec.calls
+    assert n0 == "store_kvcache" and a0[0] is k and a0[2] is attn.k_cache and a0[4] is slots
+    assert n1 == "flash_attn_varlen_func" and a1[1] is k and a1[2] is v
+    assert kw1 == dict(max_seqlen_q=5, cu_seqlens_q=cu, max_seqlen_k=5, cu_seqlens_k=cu, softmax_scale=0.125,
+                       causal=True, block_table=None)
+
+
+def test_prefill_with_block_tables_reads_the_caches(monkeypatch):
+    rec = _Recorder(monkeypatch)
+    attn = Attention(16, 128, 0.125, 2)
+    attn.k_cache, attn.v_cache = torch.zeros(2, 256, 2, 128), torch.zeros(2, 256, 2, 128)
+    bt = torch.tensor([[1, 0]], dtype=torch.int32)
+    set_context(True, torch.tensor([0, 2], dtype=torch.int32), torch.tensor([0, 300], dtype=torch.int32), 2, 300,
+                torch.tensor([298, 299], dtype=torch.int32), None, bt)
+    attn(torch.zeros(2, 16, 128), torch.zeros(2, 2, 128), torch.zeros(2, 2, 128))
+    _, a1, kw1 = rec.calls[1]
+    assert a1[1] is attn.k_cache and a1[2] is attn.v_cache and kw1["block_table"] is bt
+
+
+def test_warmup_prefill_without_caches_skips_the_store(monkeypatch):
+    rec = _Recorder(monkeypatch)
+    attn = Attention(16, 128, 0.125, 2)
+    cu = torch.tensor([0, 3], dtype=torch.int32)
+    set_context(True, cu, cu, 3, 3, torch.zeros(0, dtype=torch.int32), None, None)
+    attn(torch.zeros(3, 16, 128), torch.zeros(3, 2, 128), torch.zeros(3, 2, 128))
+    assert [c[0] for c in rec.calls] == ["flash_attn_varlen_func"]
+
+
+def test_decode_calls_the_kvcache_kernel_with_an_unsqueezed_query(monkeypatch):
+    rec = _Recorder(monkeypatch)
+    attn = Attention(16, 128, 0.125, 2)
+    attn.k_cache, attn.v_cache = torch.zeros(2, 256, 2, 128), torch.zeros(2, 256, 2, 128)
+    lens, bt = torch.tensor([7, 9], dtype=torch.int32), torch.tensor([[0], [1]], dtype=torch.int32)
+    set_context(False, slot_mapping=torch.tensor([6, 264], dtype=torch.int32), context_lens=lens, block_tables=bt)
+    attn(torch.zeros(2, 16, 128), torch.zeros(2, 2, 128), torch.zeros(2, 2, 128))
+    (n0, _, _), (n1, a1, kw1) = rec.calls
+    assert n0 == "store_kvcache" and n1 == "flash_attn_with_kvcache"
+    assert a1[0].shape == (2, 1, 16, 128) and a1[1] is attn.k_cache
+    assert kw1 == dict(cache_seqlens=lens, block_table=bt, softmax_scale=0.125, causal=True)
+
+
+def test_non_causal_calls_dense_attention(monkeypatch):
+    rec = _Recorder(monkeypatch)
+    attn = Attention(16, 128, 0.125, 2, is_causal=False)
+    attn(torch.zeros(3, 5, 16, 128), torch.zeros(3, 5, 2, 128), torch.zeros(3, 5, 2, 128))
+    assert [c[0] for c in rec.calls] == ["flash_attn_func"] and rec.calls[0][2] == dict(softmax_scale=0.125,
+                                                                                          causal=False)
+
+
+def test_context_is_read_at_call_time(monkeypatch):
+    """last_rows mutates cu_seqlens_q / max_seqlen_q of the live context around one call."""
+    rec = _Recorder(monkeypatch)
+    attn = Attention(16, 128, 0.125, 2)
+    cu = torch.tensor([0, 4, 9], dtype=torch.int32)
+    set_context(True, cu, cu, 5, 5, torch.zeros(0, dtype=torch.int32), None, None)
+    ctx = get_context()
+    ctx.cu_seqlens_q, ctx.max_seqlen_q = torch.arange(3, dtype=torch.int32), 1
+    attn(torch.zeros(2, 16, 128), torch.zeros(9, 2, 128), torch.zeros(9, 2, 128))
+    kw = rec.calls[-1][2]
+    assert kw["max_seqlen_q"] == 1 and kw["cu_seqlens_q"].tolist() == [0, 1, 2] and kw["cu_seqlens_k"] is cu
+
+
+# --- argument checks that fire before any kernel -----------------------------------------------------------------
+
+def test_store_kvcache_keeps_the_reference_asserts():
+    from voxcpm2_arabic_dialects_turbo_amd.ops import store_kvcache
+
+    k = torch.zeros(4, 2, 128, dtype=torch.bfloat16)
+    cache = torch.zeros(2, 256, 2, 128, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError):
+        store_kvcache(k, k, cache, cache, torch.zeros(3, dtype=torch.int32))  # one slot per token
+    with pytest.raises(AssertionError):
+        store_kvcache(k.transpose(1, 2).contiguous().transpose(1, 2), k, cache, cache,
+                      torch.zeros(4, dtype=torch.int32))  # last dim not contiguous
+    with pytest.raises(ValueError):
+        store_kvcache(k, k, cache, cache, torch.zeros(4, dtype=torch.int32))  # CPU tensors: not a GPU
+
+
+def test_reference_kernel_mirrors_keep_their_contracts():
+    from voxcpm2_arabic_dialects_turbo_amd.kernels.prefill_attn import paged_prefill_attention
+    from voxcpm2_arabic_dialects_turbo_amd.kernels.short_attn import short_attention, short_causal_attention
+
+    q = torch.zeros(3, 16, 128, dtype=torch.bfloat16)
+    kv = torch.zeros(3, 2, 128, dtype=torch.bfloat16)
+    cu = torch.tensor([0, 3], dtype=torch.int32)
+    with pytest.raises(AssertionError):
+        short_causal_attention(q, kv, kv, cu, 33, 0.1)  # SHORT_CAUSAL_MAX_LEN
+    with pytest.raises(NotImplementedError):
+        short_causal_attention(q, kv, kv, cu, 3, 0.1, quant=True)
+    with pytest.raises(NotImplementedError):
+        short_attention(q.view(1, 3, 16, 128), kv.view(1, 3, 2, 128), kv.view(1, 3, 2, 128), 0.1, quant=True)
+    cache = torch.zeros(2, 256, 2, 128, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError):
+        paged_prefill_attention(q, cache, cache, torch.zeros(1, 1, dtype=torch.int32), cu, cu, 3, 0.1, quant=True)

@@ -1,0 +1,175 @@
+"""GPU parity of the varlen prefill kernel (HIP kernel 2) against the oracle and the golden vectors:
+max-abs <= 2e-2, mean-abs <= 2e-3, and the reference tests' own rel 0.02 bound on their cases."""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as ref
+from tests._util import BLOCK, D, H, HK, attn_close, paged_pool, randn, uniform_lens
+from tests.golden import make_golden
+from voxcpm2_arabic_dialects_turbo_amd.kernels.prefill_attn import paged_prefill_attention
+from voxcpm2_arabic_dialects_turbo_amd.kernels.short_attn import short_attention, short_causal_attention
+from voxcpm2_arabic_dialects_turbo_amd.ops import flash_attn_func, flash_attn_varlen_func, store_kvcache
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+SCALE = D ** -0.5
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "golden.npz")
+
+
+def _golden(name):
+    return torch.from_numpy(np.load(GOLDEN, allow_pickle=False)[f"{name}__out"])
+
+
+def _cu(lens):
+    return torch.tensor([0] + np.cumsum(lens).tolist(), dtype=torch.int32)
+
+
+def test_paged_prefill_over_a_cached_prefix_reference_case():
+    """tests/test_kernel_references.py:179-207: a sequence without prefix, one with 293 cached tokens, one
+    single-token prefill after 260, through scattered 256-token pages."""
+    inp = make_golden.inputs("paged_prefill")
+    d = {k: (v.to(DEV) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    out = paged_prefill_attention(d["q"], d["k_cache"], d["v_cache"], d["tables"], d["cu_q"], d["cu_k"], 7, SCALE)
+    assert out.shape == (13, H * D) and out.dtype == torch.bfloat16
+    want = ref.varlen(inp["q"].float(), inp["cu_q"], inp["cu_k"], k_cache=inp["k_cache"], v_cache=inp["v_cache"],
+                      block_tables=inp["tables"])
+    ref.close(out.cpu(), want.view(13, -1), 0.02)
+    attn_close(out.view(13, H, D), want, "paged prefill vs oracle")
+    attn_close(out.view(13, H, D), _golden("paged_prefill"), "paged prefill vs golden")
+    # the same through flash_attn_varlen_func (Attention.forward's call)
+    out2 = flash_attn_varlen_func(d["q"], d["k_cache"], d["v_cache"], max_seqlen_q=7, cu_seqlens_q=d["cu_q"],
+                                  max_seqlen_k=300, cu_seqlens_k=d["cu_k"], softmax_scale=SCALE, causal=True,
+                                  block_table=d["tables"])
+    assert torch.equal(out2.view(13, -1), out)
+
+
+def test_short_causal_reference_case():
+    """tests/test_kernel_references.py:210-228: packed lens [1, 7, 16, 32, 3], causal over their own tokens."""
+    inp = make_golden.inputs("short_causal")
+    out = short_causal_attention(inp["q"].to(DEV), inp["k"].to(DEV), inp["v"].to(DEV), inp["cu"].to(DEV), 32, SCALE)
+    want = ref.varlen(inp["q"].float(), inp["cu"], inp["cu"], k=inp["k"], v=inp["v"])
+    ref.close(out.cpu(), want.view(59, -1), 0.02)
+    attn_close(out.view(59, H, D), want, "short causal")
+    attn_close(out.view(59, H, D)[:, make_golden.STORED_HEADS], _golden("short_causal"), "short causal vs golden")
+
+
+@pytest.mark.parametrize("L", [1, 5, 11, 16])
+def test_non_causal_short_rows(L):
+    """LocEnc / LocDiT rows (tests/test_kernel_references.py:229-237): B = 6 sequences of L tokens, non-causal."""
+    gen = torch.Generator().manual_seed(40 + L)
+    q, k, v = randn(gen, 6, L, H, D), randn(gen, 6, L, HK, D), randn(gen, 6, L, HK, D)
+    want = ref.dense(q.float(), k.float(), v.float())
+    out = short_attention(q.to(DEV), k.to(DEV), v.to(DEV), SCALE)
+    attn_close(out.view(6, L, H, D), want, f"short_attention L={L}")
+    out2 = flash_attn_func(q.to(DEV), k.to(DEV), v.to(DEV), softmax_scale=SCALE, causal=False)
+    assert out2.shape == (6, L, H, D) and torch.equal(out2.reshape(6 * L, -1), out)
+
+
+def test_dense_golden():
+    inp = make_golden.inputs("dense")
+    out = flash_attn_func(inp["q"].to(DEV), inp["k"].to(DEV), inp["v"].to(DEV), softmax_scale=SCALE)
+    attn_close(out[:, :, make_golden.STORED_HEADS], _golden("dense"), "dense vs golden")
+
+
+@pytest.mark.parametrize("mode", ["packed", "paged"])
+def test_config2_store_then_prefill(mode):
+    """8 sequences of U[64, 512] tokens packed by cu_seqlens; K/V stored into 256-token blocks of
+    a 512-block pool, then causal prefill over the step's own k / v (packed) or through the block tables (paged)."""
+    gen = torch.Generator().manual_seed(50)
+    lens = uniform_lens(gen, 8, 64, 512)
+    T = sum(lens)
+    kc, vc, tables = paged_pool(gen, lens, 512)
+    qkv = randn(gen, T, (H + 2 * HK) * D).to(DEV)
+    q, k, v = qkv.split([H * D, HK * D, HK * D], dim=-1)
+    q, k, v = q.view(T, H, D), k.view(T, HK, D), v.view(T, HK, D)
+    slots = torch.cat([torch.tensor([ref.slot_of(tables[b].tolist(), j, BLOCK) for j in range(n)])
+                       for b, n in enumerate(lens)]).to(torch.int32)
+    kc_d, vc_d = kc.to(DEV), vc.to(DEV)
+    store_kvcache(k, v, kc_d, vc_d, slots.to(DEV))
+    cu = _cu(lens).to(DEV)
+    if mode == "packed":
+        out = flash_attn_varlen_func(q, k, v, max(lens), cu, max(lens), cu, softmax_scale=SCALE, causal=True)
+    else:
+        out = flash_attn_varlen_func(q, kc_d, vc_d, max(lens), cu, max(lens), cu, softmax_scale=SCALE, causal=True,
+                                     block_table=tables.to(DEV))
+    want = ref.varlen(q.float().cpu(), _cu(lens), _cu(lens), k=k.cpu(), v=v.cpu())
+    attn_close(out, want, f"config 2 {mode}")
+
+
+def test_config5_mixed_prefill_and_decode_rows():
+    """one varlen paged call with 6 new prefills (U[300, 600] tokens, stored first) and 120 decode
+    rows (one query over U[128, 1800] cached tokens), 2048-block pool."""
+    gen = torch.Generator().manual_seed(51)
+    pre = uniform_lens(gen, 6, 300, 600)
+    dec = uniform_lens(gen, 120, 128, 1800)
+    nk = pre + dec
+    nq = pre + [1] * 120
+    kc, vc, tables = paged_pool(gen, nk, 2048)
+    Tq = sum(nq)
+    q = randn(gen, Tq, H, D)
+    k_new, v_new = randn(gen, sum(pre), HK, D), randn(gen, sum(pre), HK, D)
+    slots = torch.cat([torch.tensor([ref.slot_of(tables[b].tolist(), j, BLOCK) for j in range(n)])
+                       for b, n in enumerate(pre)]).to(torch.int32)
+    kc_d, vc_d = kc.to(DEV), vc.to(DEV)
+    store_kvcache(k_new.to(DEV), v_new.to(DEV), kc_d, vc_d, slots.to(DEV))
+    ref.store_kvcache(k_new, v_new, kc, vc, slots)
+    out = flash_attn_varlen_func(q.to(DEV), kc_d, vc_d, max(nq), _cu(nq).to(DEV), max(nk), _cu(nk).to(DEV),
+                                 softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
+    want = ref.varlen(q.float(), _cu(nq), _cu(nk), k_cache=kc, v_cache=vc, block_tables=tables)
+    attn_close(out, want, "config 5")
+
+
+def test_last_rows_one_query_per_sequence_over_all_keys():
+    """The residual LM's last layer (kernels/fused_layer.py:767-773): cu_seqlens_q = arange(n + 1), max_seqlen_q = 1,
+    keys = every row of the step (packed, cu_seqlens_k)."""
+    gen = torch.Generator().manual_seed(52)
+    lens = [5, 33, 1, 200]
+    T = sum(lens)
+    k, v = randn(gen, T, HK, D), randn(gen, T, HK, D)
+    q_last = randn(gen, len(lens), H, D)
+    cu_q = torch.arange(len(lens) + 1, dtype=torch.int32)
+    out = flash_attn_varlen_func(q_last.to(DEV), k.to(DEV), v.to(DEV), 1, cu_q.to(DEV), max(lens),
+                                 _cu(lens).to(DEV), softmax_scale=SCALE, causal=True)
+    want = ref.varlen(q_last.float(), cu_q, _cu(lens), k=k, v=v)
+    attn_close(out, want, "last rows")
+
+
+def test_zero_length_sequences_in_a_padded_batch():
+    """A captured prefill bucket pads with zero-length sequences; they produce no rows and disturb nothing."""
+    gen = torch.Generator().manual_seed(53)
+    nq = [0, 17, 0, 0, 64, 0]
+    nk = [0, 17, 0, 0, 300, 0]
+    kc, vc, tables = paged_pool(gen, [max(n, 1) for n in nk], 16)
+    q = randn(gen, sum(nq), H, D)
+    out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), 64, _cu(nq).to(DEV), 300, _cu(nk).to(DEV),
+                                 softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
+    want = ref.varlen(q.float(), _cu(nq), _cu(nk), k_cache=kc, v_cache=vc, block_tables=tables)
+    attn_close(out, want, "zero-length sequences")
+
+
+@pytest.mark.parametrize("h,hk", [(16, 1), (8, 1), (16, 4), (4, 4)])
+def test_group_sizes(h, hk):
+    gen = torch.Generator().manual_seed(54 + h + hk)
+    lens = [1, 70, 129, 33]
+    T = sum(lens)
+    q, k, v = randn(gen, T, h, D), randn(gen, T, hk, D), randn(gen, T, hk, D)
+    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), max(lens), _cu(lens).to(DEV), max(lens),
+                                 _cu(lens).to(DEV), softmax_scale=SCALE, causal=True)
+    attn_close(out, ref.varlen(q.float(), _cu(lens), _cu(lens), k=k, v=v), f"H={h} HK={hk}")
+
+
+def test_long_sequences_compute_bound_shape():
+    """Longer sequences (the compute-bound prefill shape the bench also reports): 4 x U[1024, 2048] tokens."""
+    gen = torch.Generator().manual_seed(55)
+    lens = uniform_lens(gen, 4, 1024, 2048)
+    T = sum(lens)
+    q, k, v = randn(gen, T, H, D), randn(gen, T, HK, D), randn(gen, T, HK, D)
+    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), max(lens), _cu(lens).to(DEV), max(lens),
+                                 _cu(lens).to(DEV), softmax_scale=SCALE, causal=True)
+    attn_close(out, ref.varlen(q.float(), _cu(lens), _cu(lens), k=k, v=v), "long causal")

@@ -1,0 +1,204 @@
+// C-ABI entry points of libvoxattn.so (declared in include/vox_attn.h).
+//
+// Every entry point validates its arguments on the host, launches on the caller's stream, checks the launch, and
+// returns a status (VOX_OK, VOX_EINVAL, VOX_EHIP) instead of throwing; vox_last_error() gives the calling thread's
+// message for the last failure. Nothing here allocates, frees or synchronizes, so every call can be captured into
+// a HIP graph.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "vox_kernels.h"
+#include "../../include/vox_attn.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+int g_decode_chunk_override = 0;
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return VOX_OK;
+  return fail(VOX_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+constexpr int kHeadDim = 128;
+constexpr int kMaxHeads = 16;
+
+}  // namespace
+
+extern "C" {
+
+const char* vox_last_error(void) { return g_err; }
+
+int vox_abi_version(void) { return VOX_ABI_VERSION; }
+
+int vox_store_kvcache(const void* key, const void* value, int64_t key_row_stride, int64_t value_row_stride,
+                      void* k_cache, void* v_cache, int64_t num_slots, const int32_t* slot_mapping,
+                      int64_t num_tokens, int num_kv_heads, int head_dim, void* stream) {
+  if (num_tokens < 0) return fail(VOX_EINVAL, "store_kvcache: num_tokens %lld < 0", (long long)num_tokens);
+  if (num_tokens == 0) return VOX_OK;
+  if (!key || !value || !k_cache || !v_cache || !slot_mapping)
+    return fail(VOX_EINVAL, "store_kvcache: null pointer argument");
+  if (num_kv_heads <= 0 || head_dim <= 0) return fail(VOX_EINVAL, "store_kvcache: bad head shape");
+  if (num_slots <= 0) return fail(VOX_EINVAL, "store_kvcache: empty cache");
+  const int row = num_kv_heads * head_dim;
+  if (key_row_stride < row || value_row_stride < row)
+    return fail(VOX_EINVAL, "store_kvcache: row stride smaller than num_kv_heads * head_dim");
+  const bool vec16 = (row % 8 == 0) && (key_row_stride % 8 == 0) && (value_row_stride % 8 == 0) &&
+                     aligned16(key) && aligned16(value) && aligned16(k_cache) && aligned16(v_cache);
+  return hip_status(vox::launch_store_kvcache(key, value, key_row_stride, value_row_stride, k_cache, v_cache,
+                                              num_slots, slot_mapping, num_tokens, row, vec16,
+                                              (hipStream_t)stream),
+                    "store_kvcache launch");
+}
+
+int vox_decode_chunk_tokens(int batch, int max_blocks, int block_size) {
+  if (g_decode_chunk_override > 0) return g_decode_chunk_override;
+  return vox::decode_chunk_tokens(batch, max_blocks * block_size);
+}
+
+void vox_set_decode_chunk_tokens(int tokens) { g_decode_chunk_override = tokens > 0 ? tokens : 0; }
+
+size_t vox_decode_workspace_bytes(int batch, int max_blocks, int block_size) {
+  if (batch <= 0 || max_blocks <= 0 || block_size <= 0) return 0;
+  const int chunk = vox_decode_chunk_tokens(batch, max_blocks, block_size);
+  const int64_t max_ctx = (int64_t)max_blocks * block_size;
+  const int64_t max_chunks = (max_ctx + chunk - 1) / chunk;
+  return (size_t)batch * (size_t)max_chunks * vox::kPartialFloats * sizeof(float);
+}
+
+int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
+                    int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
+                    int max_blocks, const int32_t* context_lens, int batch, int num_heads, int num_kv_heads,
+                    int head_dim, float softmax_scale, void* workspace, size_t workspace_bytes, int32_t* counters,
+                    int64_t num_counters, void* out, void* stream) {
+  if (batch < 0) return fail(VOX_EINVAL, "decode_attn: batch < 0");
+  if (batch == 0) return VOX_OK;
+  if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out || !counters)
+    return fail(VOX_EINVAL, "decode_attn: null pointer argument");
+  if (head_dim != kHeadDim) return fail(VOX_EINVAL, "decode_attn: head_dim %d unsupported (128 only)", head_dim);
+  if (num_kv_heads != 1 && num_kv_heads != 2)
+    return fail(VOX_EINVAL, "decode_attn: num_kv_heads %d unsupported (1 or 2)", num_kv_heads);
+  if (num_heads <= 0 || num_heads > kMaxHeads || num_heads % num_kv_heads)
+    return fail(VOX_EINVAL, "decode_attn: num_heads %d must be <= 16 and a multiple of num_kv_heads", num_heads);
+  if (block_size <= 0 || block_size % 32)
+    return fail(VOX_EINVAL, "decode_attn: block_size %d must be a positive multiple of 32", block_size);
+  if (max_blocks <= 0 || bt_stride < max_blocks) return fail(VOX_EINVAL, "decode_attn: bad block table shape");
+  if (num_blocks <= 0) return fail(VOX_EINVAL, "decode_attn: empty cache");
+  if (q_row_stride < (int64_t)num_heads * head_dim || q_row_stride % 8)
+    return fail(VOX_EINVAL, "decode_attn: q row stride %lld", (long long)q_row_stride);
+  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out) || !aligned16(workspace))
+    return fail(VOX_EINVAL, "decode_attn: q, caches, out and workspace must be 16-byte aligned");
+  if (num_counters < batch) return fail(VOX_EINVAL, "decode_attn: %lld counters for batch %d",
+                                        (long long)num_counters, batch);
+  if (!std::isfinite(softmax_scale)) return fail(VOX_EINVAL, "decode_attn: softmax_scale is not finite");
+  const size_t need = vox_decode_workspace_bytes(batch, max_blocks, block_size);
+  if (workspace_bytes < need || (need && !workspace))
+    return fail(VOX_EINVAL, "decode_attn: workspace of %zu bytes, %zu needed", workspace_bytes, need);
+  const int chunk = vox_decode_chunk_tokens(batch, max_blocks, block_size);
+  if (chunk <= 0 || chunk % 128) return fail(VOX_EINVAL, "decode_attn: chunk %d not a multiple of 128", chunk);
+  const int max_ctx = max_blocks * block_size;
+
+  vox::DecodeArgs a;
+  a.q = (const uint16_t*)q;
+  a.q_row_stride = q_row_stride;
+  a.k_cache = (const uint16_t*)k_cache;
+  a.v_cache = (const uint16_t*)v_cache;
+  a.num_blocks = num_blocks;
+  a.block_size = block_size;
+  a.block_tables = block_tables;
+  a.bt_stride = bt_stride;
+  a.max_blocks = max_blocks;
+  a.context_lens = context_lens;
+  a.batch = batch;
+  a.num_heads = num_heads;
+  a.group = num_heads / num_kv_heads;
+  a.scale_log2 = softmax_scale * 1.4426950408889634f;
+  a.chunk = chunk;
+  a.max_chunks = (max_ctx + chunk - 1) / chunk;
+  a.partials = (float*)workspace;
+  a.counters = counters;
+  a.out = (uint16_t*)out;
+  return hip_status(vox::launch_decode(a, num_kv_heads, max_ctx, (hipStream_t)stream), "decode_attn launch");
+}
+
+int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const void* value,
+                     int64_t key_row_stride, int64_t value_row_stride, const void* k_cache, const void* v_cache,
+                     int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
+                     int max_blocks, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch,
+                     int max_seqlen_q, int uniform_seqlen_q, int uniform_seqlen_k, int num_heads, int num_kv_heads,
+                     int head_dim, float softmax_scale, int causal, void* out, int64_t out_row_stride,
+                     void* stream) {
+  if (batch < 0 || max_seqlen_q < 0) return fail(VOX_EINVAL, "prefill_attn: negative batch or max_seqlen_q");
+  if (batch == 0 || max_seqlen_q == 0) return VOX_OK;
+  if (!q || !out) return fail(VOX_EINVAL, "prefill_attn: null q or out");
+  if (head_dim != kHeadDim) return fail(VOX_EINVAL, "prefill_attn: head_dim %d unsupported (128 only)", head_dim);
+  if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads)
+    return fail(VOX_EINVAL, "prefill_attn: num_heads %d not a multiple of num_kv_heads %d", num_heads,
+                num_kv_heads);
+  const int group = num_heads / num_kv_heads;
+  if (128 % group) return fail(VOX_EINVAL, "prefill_attn: group size %d must divide 128", group);
+  if ((cu_seqlens_q == nullptr) != (cu_seqlens_k == nullptr))
+    return fail(VOX_EINVAL, "prefill_attn: give both cu_seqlens or neither");
+  if (!cu_seqlens_q && (uniform_seqlen_q <= 0 || uniform_seqlen_k <= 0))
+    return fail(VOX_EINVAL, "prefill_attn: uniform lengths must be positive without cu_seqlens");
+  if (!cu_seqlens_q && max_seqlen_q != uniform_seqlen_q)
+    return fail(VOX_EINVAL, "prefill_attn: max_seqlen_q must equal the uniform length");
+  if (q_row_stride < (int64_t)num_heads * head_dim || q_row_stride % 8 || !aligned16(q))
+    return fail(VOX_EINVAL, "prefill_attn: q must be 16-byte aligned with a row stride >= H*D, multiple of 8");
+  if (out_row_stride < (int64_t)num_heads * head_dim || out_row_stride % 4 || ((uintptr_t)out & 7u))
+    return fail(VOX_EINVAL, "prefill_attn: bad out row stride or alignment");
+  if (!std::isfinite(softmax_scale)) return fail(VOX_EINVAL, "prefill_attn: softmax_scale is not finite");
+  if (block_tables) {
+    if (!k_cache || !v_cache) return fail(VOX_EINVAL, "prefill_attn: block tables without caches");
+    if (block_size <= 0 || max_blocks <= 0 || bt_stride < max_blocks || num_blocks <= 0)
+      return fail(VOX_EINVAL, "prefill_attn: bad block table or cache shape");
+    if (!aligned16(k_cache) || !aligned16(v_cache)) return fail(VOX_EINVAL, "prefill_attn: caches not aligned");
+  } else {
+    if (!key || !value) return fail(VOX_EINVAL, "prefill_attn: null key/value without block tables");
+    if (key_row_stride < (int64_t)num_kv_heads * head_dim || value_row_stride < (int64_t)num_kv_heads * head_dim ||
+        key_row_stride % 8 || value_row_stride % 8 || !aligned16(key) || !aligned16(value))
+      return fail(VOX_EINVAL, "prefill_attn: key/value must be 16-byte aligned rows, stride multiple of 8");
+  }
+
+  vox::PrefillArgs a;
+  a.q = (const uint16_t*)q;
+  a.q_row_stride = q_row_stride;
+  a.k_src = (const uint16_t*)key;
+  a.v_src = (const uint16_t*)value;
+  a.k_row_stride = key_row_stride;
+  a.v_row_stride = value_row_stride;
+  a.k_cache = (const uint16_t*)k_cache;
+  a.v_cache = (const uint16_t*)v_cache;
+  a.num_blocks = num_blocks;
+  a.block_size = block_size;
+  a.block_tables = block_tables;
+  a.bt_stride = bt_stride;
+  a.max_blocks = max_blocks;
+  a.cu_q = cu_seqlens_q;
+  a.cu_k = cu_seqlens_k;
+  a.uniform_q = uniform_seqlen_q;
+  a.uniform_k = uniform_seqlen_k;
+  a.batch = batch;
+  a.num_heads = num_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.group = group;
+  a.scale_log2 = softmax_scale * 1.4426950408889634f;
+  a.causal = causal ? 1 : 0;
+  a.out = (uint16_t*)out;
+  a.out_row_stride = out_row_stride;
+  return hip_status(vox::launch_prefill(a, max_seqlen_q, (hipStream_t)stream), "prefill_attn launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,229 @@
+// Kernel 2: varlen (optionally causal) GQA attention for prefill steps, on bf16 MFMA.
+//
+// Semantics (reference calls: nanovllm_voxcpm/model/layers.py:337-348 flash_attn_varlen_func, with or without
+// block_table; :361 flash_attn_func for the non-causal short rows; the Triton paged_prefill_attention and
+// short_causal_attention of nanovllm_voxcpm/kernels/prefill_attn.py:20-124 and kernels/short_attn.py:95-179):
+// sequence b has nq = cu_q[b+1] - cu_q[b] queries and nk = cu_k[b+1] - cu_k[b] keys; with `causal` query i sees keys
+// j <= nk - nq + i (bottom-right aligned), o = softmax(scale * q k^T) v in fp32, stored as bf16. Keys come from the
+// paged cache through block_tables, or from packed [Tk, HK, D] rows when there is no block table.
+//
+// gfx950 mapping. A workgroup (4 waves, 256 threads) owns 128 query rows = (128 / G tokens) x (the G query heads of
+// one kv head): GQA shares every K/V tile across the group's heads. Per 64-key tile the workgroup stages K
+// row-major and V transposed ([d][key]) in LDS; each wave computes S^T[64 keys x 32 rows] = K Q^T with Q^T held in
+// registers, an online softmax in fp32 (exp2, log2-prescaled scale), and O^T[128 d x 32 rows] += V^T P^T, where P^T
+// comes out of the score MFMA already in B-operand layout.
+#include "vox_common.h"
+#include "vox_kernels.h"
+
+namespace vox {
+
+namespace {
+
+constexpr int kD = 128;
+constexpr int kBK = 64;          // keys per tile
+constexpr int kRows = 128;       // query rows per workgroup
+constexpr int kKsStride = kD + 8;   // LDS K row: 128 d + 8 pad (bf16)
+constexpr int kVtStride = kBK + 8;  // LDS V^T row: 64 keys + 8 pad (bf16)
+
+__global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs p) {
+  __shared__ __attribute__((aligned(16))) uint16_t ks[kBK][kKsStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vts[kD][kVtStride];
+
+  const int qt = blockIdx.x;
+  const int b = blockIdx.y;
+  const int g = blockIdx.z;
+  int q0, nq, k0, nk;
+  if (p.cu_q) {
+    q0 = p.cu_q[b];
+    nq = p.cu_q[b + 1] - q0;
+  } else {
+    q0 = b * p.uniform_q;
+    nq = p.uniform_q;
+  }
+  if (p.cu_k) {
+    k0 = p.cu_k[b];
+    nk = p.cu_k[b + 1] - k0;
+  } else {
+    k0 = b * p.uniform_k;
+    nk = p.uniform_k;
+  }
+  if (p.block_tables) nk = min(nk, p.max_blocks * p.block_size);  // keys the block table can address
+  const int G = p.group;
+  const int BQ = kRows / G;  // query tokens per workgroup
+  if (qt * BQ >= nq) return;
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6;
+  const int lane = tid & 63;
+  const int r16 = lane & 15;
+  const int jq = lane >> 4;
+  const int HK = p.num_kv_heads;
+
+  // This lane's two query rows (one per 16-row MFMA column tile): rho = w*32 + rt*16 + r16.
+  u32x4 qop[2][4];
+  bool row_ok[2];
+  int qpos[2];
+  int tq_of[2];
+  int h_of[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int rho = w * 32 + rt * 16 + r16;
+    const int tq = qt * BQ + rho / G;
+    const int h = g * G + rho % G;
+    tq_of[rt] = tq;
+    h_of[rt] = h;
+    row_ok[rt] = tq < nq;
+    qpos[rt] = nk - nq + tq;
+    const uint16_t* qp = p.q + (int64_t)(q0 + tq) * p.q_row_stride + (int64_t)h * kD + jq * 8;
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) qop[rt][kc] = row_ok[rt] ? ld_g16(qp + kc * 32) : zero4();
+  }
+
+  const int tq_last = min(nq, (qt + 1) * BQ) - 1;
+  const int kv_end = p.causal ? min(nk, nk - nq + tq_last + 1) : nk;
+
+  float m[2] = {-INFINITY, -INFINITY};
+  float l[2] = {0.f, 0.f};
+  f32x4 acc[8][2];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) acc[dt][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int kv0 = 0; kv0 < kv_end; kv0 += kBK) {
+    // ---- stage the K (row-major) and V (transposed) tiles of kv head g ----
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int pc = tid + i * 256;
+      const int kk = pc >> 4;
+      const int dc = (pc & 15) * 8;
+      const int jj = kv0 + kk;
+      u32x4 kv = zero4(), vv = zero4();
+      if (jj < nk) {
+        const uint16_t* kp = nullptr;
+        const uint16_t* vp = nullptr;
+        if (p.block_tables) {
+          const int col = jj / p.block_size;
+          const int64_t blk = p.block_tables[(int64_t)b * p.bt_stride + col];
+          if (blk >= 0 && blk < p.num_blocks) {
+            const int64_t off = ((blk * p.block_size + jj % p.block_size) * HK + g) * kD + dc;
+            kp = p.k_cache + off;
+            vp = p.v_cache + off;
+          }
+        } else {
+          kp = p.k_src + (int64_t)(k0 + jj) * p.k_row_stride + g * kD + dc;
+          vp = p.v_src + (int64_t)(k0 + jj) * p.v_row_stride + g * kD + dc;
+        }
+        if (kp) {
+          kv = ld_g16(kp);
+          vv = ld_g16(vp);
+        }
+      }
+      *reinterpret_cast<u32x4*>(&ks[kk][dc]) = kv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vts[dc + 2 * e][kk] = (uint16_t)(vv[e] & 0xffffu);
+        vts[dc + 2 * e + 1][kk] = (uint16_t)(vv[e] >> 16);
+      }
+    }
+    __syncthreads();
+
+    // ---- S^T[key][row] = K Q^T ----
+    f32x4 s[4][2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      s[kt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+      s[kt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(&ks[kt * 16 + r16][kc * 32 + jq * 8]);
+        s[kt][0] = mfma_16x16x32(a, qop[0][kc], s[kt][0]);
+        s[kt][1] = mfma_16x16x32(a, qop[1][kc], s[kt][1]);
+      }
+    }
+
+    // ---- masked online softmax, one row per lane column ----
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int jj = kv0 + kt * 16 + jq * 4 + rr;
+          const bool ok = jj < nk && (!p.causal || jj <= qpos[rt]);
+          const float x = ok ? s[kt][rt][rr] * p.scale_log2 : -INFINITY;
+          s[kt][rt][rr] = x;
+          tmax = fmaxf(tmax, x);
+        }
+      tmax = col_max4(tmax);
+      const float m_new = fmaxf(m[rt], tmax);
+      const float mu = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = fast_exp2(m[rt] - mu);
+      float ps = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const float e = fast_exp2(s[kt][rt][rr] - mu);
+          s[kt][rt][rr] = e;
+          ps += e;
+        }
+      l[rt] = l[rt] * alpha + ps;
+      m[rt] = m_new;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) acc[dt][rt] *= alpha;
+    }
+
+    // ---- O^T[d][row] += V^T P^T; k-step ks covers keys ks*32 + [0, 32) ----
+    u32x4 pb[2][2];
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+        pb[k2][rt] = u32x4{pack_bf16x2(s[2 * k2][rt][0], s[2 * k2][rt][1]),
+                           pack_bf16x2(s[2 * k2][rt][2], s[2 * k2][rt][3]),
+                           pack_bf16x2(s[2 * k2 + 1][rt][0], s[2 * k2 + 1][rt][1]),
+                           pack_bf16x2(s[2 * k2 + 1][rt][2], s[2 * k2 + 1][rt][3])};
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2) {
+        const uint16_t* row = &vts[dt * 16 + r16][k2 * 32];
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(row + jq * 4);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(row + 16 + jq * 4);
+        const u32x4 a = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        acc[dt][0] = mfma_16x16x32(a, pb[k2][0], acc[dt][0]);
+        acc[dt][1] = mfma_16x16x32(a, pb[k2][1], acc[dt][1]);
+      }
+    __syncthreads();
+  }
+
+  // ---- epilogue: normalize, bf16, 4 consecutive dims per lane per d-tile ----
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const float L = col_sum4(l[rt]);
+    if (!row_ok[rt]) continue;
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    uint16_t* op = p.out + (int64_t)(q0 + tq_of[rt]) * p.out_row_stride + (int64_t)h_of[rt] * kD + jq * 4;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const f32x4 v = acc[dt][rt];
+      *reinterpret_cast<u32x2*>(op + dt * 16) =
+          u32x2{pack_bf16x2(v[0] * inv, v[1] * inv), pack_bf16x2(v[2] * inv, v[3] * inv)};
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_prefill(const PrefillArgs& a, int max_seqlen_q, hipStream_t stream) {
+  const int bq = kRows / a.group;
+  const int q_tiles = (max_seqlen_q + bq - 1) / bq;
+  if (q_tiles <= 0 || a.batch <= 0) return hipSuccess;
+  dim3 grid((unsigned)q_tiles, (unsigned)a.batch, (unsigned)a.num_kv_heads);
+  prefill_kernel<<<grid, dim3(256), 0, stream>>>(a);
+  return hipGetLastError();
+}
+
+}  // namespace vox

@@ -1,0 +1,68 @@
+// Shared device helpers for the gfx950 paged-KV attention kernels.
+//
+// Everything here is written for CDNA4 (gfx950, wave64): bf16 MFMA 16x16x32, 16-byte vector memory
+// operations and cross-lane reductions within one 64-lane wavefront.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vox {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// D(16x16 fp32) += A(16x32 bf16) * B(32x16 bf16).
+// Lane l holds A[row = l%16][k = 8*(l/16) .. +8), B[k = 8*(l/16) .. +8)[col = l%16] and
+// D[row = 4*(l/16) .. +4][col = l%16]. Which physical k a register slot stands for is free as long as A and B
+// agree, which the kernels use to feed operands straight from memory.
+__device__ __forceinline__ f32x4 mfma_16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+
+__device__ __forceinline__ u32x4 zero4() { return u32x4{0u, 0u, 0u, 0u}; }
+
+// 16-byte global load (one dwordx4 per lane).
+__device__ __forceinline__ u32x4 ld_g16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// Round-to-nearest-even fp32 -> bf16 of two values packed low/high into one dword.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  __bf16 a = static_cast<__bf16>(lo);
+  __bf16 b = static_cast<__bf16>(hi);
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+}
+
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t bits16) {
+  return __builtin_bit_cast(float, bits16 << 16);
+}
+
+// Max / sum over the four lanes {l, l^16, l^32, l^48} that share l%16 (one MFMA column).
+__device__ __forceinline__ float col_max4(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16, kWave));
+  x = fmaxf(x, __shfl_xor(x, 32, kWave));
+  return x;
+}
+__device__ __forceinline__ float col_sum4(float x) {
+  x += __shfl_xor(x, 16, kWave);
+  x += __shfl_xor(x, 32, kWave);
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Orders this wavefront's LDS writes before its later LDS reads of other lanes' data (wave-private buffers).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+}  // namespace vox

@@ -1,0 +1,74 @@
+// Launch descriptors shared by the kernels and the C-ABI layer (host and device visible, plain data only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vox {
+
+// One decode partial per (sequence, chunk): O[16 heads][128] unnormalized, then m[16] and l[16] (log2 domain).
+constexpr int kPartialFloats = 16 * 128 + 16 + 16;
+
+struct DecodeArgs {
+  const uint16_t* q;          // bf16 [B, H, 128]; sequence rows q_row_stride apart, heads 128 apart
+  int64_t q_row_stride;
+  const uint16_t* k_cache;    // bf16 [num_blocks, block_size, HK, 128], contiguous
+  const uint16_t* v_cache;
+  int64_t num_blocks;
+  int block_size;
+  const int32_t* block_tables;  // int32 [B, bt_stride], first max_blocks columns used
+  int64_t bt_stride;
+  int max_blocks;
+  const int32_t* context_lens;  // int32 [B]
+  int batch;
+  int num_heads;
+  int group;                  // H / HK
+  float scale_log2;           // softmax_scale * log2(e)
+  int chunk;                  // tokens per workgroup (multiple of 128)
+  int max_chunks;             // ceil(max_blocks * block_size / chunk)
+  float* partials;            // [B, max_chunks, kPartialFloats]
+  int32_t* counters;          // [B], zero on entry, zero again on exit
+  uint16_t* out;              // bf16 [B, H, 128], contiguous
+};
+
+struct PrefillArgs {
+  const uint16_t* q;          // bf16 [T, H, 128]; token rows q_row_stride apart
+  int64_t q_row_stride;
+  // packed K/V (block_tables == nullptr): bf16 [Tk, HK, 128], token rows *_row_stride apart
+  const uint16_t* k_src;
+  const uint16_t* v_src;
+  int64_t k_row_stride;
+  int64_t v_row_stride;
+  // paged K/V (block_tables != nullptr): bf16 [num_blocks, block_size, HK, 128], contiguous
+  const uint16_t* k_cache;
+  const uint16_t* v_cache;
+  int64_t num_blocks;
+  int block_size;
+  const int32_t* block_tables;
+  int64_t bt_stride;
+  int max_blocks;
+  // sequences: cu_seqlens (int32 [B + 1]) or, when null, uniform lengths
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  int uniform_q;
+  int uniform_k;
+  int batch;
+  int num_heads;
+  int num_kv_heads;
+  int group;                  // H / HK; 128 % group == 0
+  float scale_log2;
+  int causal;                 // bottom-right aligned: query i of nq sees keys j <= nk - nq + i
+  uint16_t* out;              // bf16 [T, H, 128]; token rows out_row_stride apart
+  int64_t out_row_stride;
+};
+
+hipError_t launch_store_kvcache(const void* k, const void* v, int64_t k_row_stride, int64_t v_row_stride,
+                                void* k_cache, void* v_cache, int64_t num_slots, const int32_t* slot_mapping,
+                                int64_t n, int row_elems, bool vec16, hipStream_t stream);
+
+int decode_chunk_tokens(int batch, int max_ctx);
+hipError_t launch_decode(const DecodeArgs& a, int num_kv_heads, int max_ctx, hipStream_t stream);
+
+hipError_t launch_prefill(const PrefillArgs& a, int max_seqlen_q, hipStream_t stream);
+
+}  // namespace vox

@@ -1,0 +1,81 @@
+"""The drop-in attention module of the VoxCPM2 engine's causal and non-causal layers.
+
+``Attention`` keeps the reference module's constructor, public attributes (``num_heads``, ``head_dim``, ``scale``,
+``num_kv_heads``, ``is_causal`` and the assignable ``k_cache`` / ``v_cache`` that a runner sets to per-layer views
+``kv[i, 0]`` / ``kv[i, 1]`` of one [layers, 2, num_blocks, block_size, HK, head_dim] allocation) and its
+``forward(q, k, v)`` dispatch, reading the forward context at call time
+(reference: nanovllm_voxcpm/model/layers.py:308-362):
+
+- causal, caches allocated: store this step's K/V at ``slot_mapping`` first;
+- causal prefill: varlen attention over the step's own k / v, or over the caches when ``block_tables`` is set
+  (prefix cache, mixed prefill + decode steps, prefill graphs), bottom-right causal;
+- causal decode: paged split-KV decode over ``context_lens`` / ``block_tables``; returns [B, 1, H, D];
+- non-causal: dense attention over [B, L, H, D] (LocEnc / LocDiT rows).
+
+Every branch runs a HIP kernel of libvoxattn.so; nothing here synchronizes or allocates outside torch, so the
+module can be captured into HIP graphs exactly where the reference captures its decode step.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from .context import get_context
+from .ops import flash_attn_func, flash_attn_varlen_func, flash_attn_with_kvcache, store_kvcache
+
+__all__ = ["Attention", "store_kvcache"]
+
+
+class Attention(nn.Module):
+
+    def __init__(
+        self,
+        num_heads,
+        head_dim,
+        scale,
+        num_kv_heads,
+        is_causal: bool = True,
+    ):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.scale = scale
+        self.num_kv_heads = num_kv_heads
+        self.k_cache = self.v_cache = torch.tensor([])
+        self.is_causal = is_causal
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
+        if self.is_causal:
+            context = get_context()
+            k_cache, v_cache = self.k_cache, self.v_cache
+            if k_cache.numel() and v_cache.numel():
+                store_kvcache(k, v, k_cache, v_cache, context.slot_mapping)
+            if context.is_prefill:
+                if context.block_tables is not None:  # prefix cache: keys through the block tables
+                    k, v = k_cache, v_cache
+                o = flash_attn_varlen_func(
+                    q,
+                    k,
+                    v,
+                    max_seqlen_q=context.max_seqlen_q,
+                    cu_seqlens_q=context.cu_seqlens_q,
+                    max_seqlen_k=context.max_seqlen_k,
+                    cu_seqlens_k=context.cu_seqlens_k,
+                    softmax_scale=self.scale,
+                    causal=True,
+                    block_table=context.block_tables,
+                )
+            else:  # decode
+                o = flash_attn_with_kvcache(
+                    q.unsqueeze(1),
+                    k_cache,
+                    v_cache,
+                    cache_seqlens=context.context_lens,
+                    block_table=context.block_tables,
+                    softmax_scale=self.scale,
+                    causal=True,
+                )
+        else:  # non-causal, no KV cache
+            o = flash_attn_func(q, k, v, softmax_scale=self.scale, causal=False)
+        return o

@@ -1,0 +1,284 @@
+"""The attention operators the reference's Attention.forward calls, on the gfx950 kernels of libvoxattn.so.
+
+Names, argument meanings, shapes and returned layouts follow the calls the reference makes
+(reference: nanovllm_voxcpm/model/layers.py:290-305 store_kvcache, :337-348 flash_attn_varlen_func,
+:350-358 flash_attn_with_kvcache, :361 flash_attn_func). Every op runs on torch's current stream, allocates its
+outputs with torch (graph-pool safe), never synchronizes, and raises when libvoxattn.so is missing: there is no
+CPU or PyTorch fallback.
+
+Supported shapes are the model's: head_dim 128, bf16 activations and caches (any 2-byte dtype for the KV store),
+int32 index tensors. Decode takes up to 16 query heads over 1 or 2 KV heads.
+"""
+
+from __future__ import annotations
+
+import threading
+
+import torch
+
+from . import _lib
+
+HEAD_DIM = 128
+MAX_DECODE_HEADS = 16
+DECODE_COUNTERS = 1 << 16  # arrival counters per device: the largest decode batch one launch may take
+
+_counters: dict[int, torch.Tensor] = {}
+_counters_lock = threading.Lock()
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise AssertionError(msg)
+
+
+def _check_cuda(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    for t in tensors:
+        if t is not None and (t.device.type != "cuda" or t.device != dev):
+            raise ValueError(f"all tensors must be on the same GPU, got {t.device} and {dev}")
+    return dev
+
+
+def _as_i32(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dtype == torch.int32:
+        return t if t.is_contiguous() else t.contiguous()
+    if t.dtype in (torch.int64, torch.int16, torch.uint8, torch.int8):
+        return t.to(torch.int32).contiguous()
+    raise TypeError(f"{name} must be an integer tensor, got {t.dtype}")
+
+
+def decode_counters(device: torch.device) -> torch.Tensor:
+    """The device's persistent int32 arrival counters of the split-KV decode (all zero between launches).
+
+    Created zero-filled on first use outside graph capture; every decode launch leaves them zero again. Launches on
+    one device that share them must be ordered on one stream (the reference runs each engine on one stream)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    t = _counters.get(idx)
+    if t is not None:
+        return t
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(
+            "decode_attn: its arrival counters must be created by an eager decode call before graph capture "
+            "(run the warm-up step first, or call ops.decode_counters(device) before capturing)"
+        )
+    with _counters_lock:
+        t = _counters.get(idx)
+        if t is None:
+            t = torch.zeros(DECODE_COUNTERS, dtype=torch.int32, device=torch.device("cuda", idx))
+            _counters[idx] = t
+    return t
+
+
+# --------------------------------------------------------------------------------------------------------------------
+# KV store
+
+
+def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                  slot_mapping: torch.Tensor) -> None:
+    """Writes key[i] / value[i] ([N, HK, head_dim], token rows may be strided) to the cache slot slot_mapping[i];
+    slot -1 is skipped. Caches are [num_blocks, block_size, HK, head_dim] (or any view whose slot rows are
+    HK * head_dim apart). Bit-exact. Reference: nanovllm_voxcpm/model/layers.py:290-305 (same asserts)."""
+    N, num_heads, head_dim = key.shape
+    D = num_heads * head_dim
+    _require(key.stride(-1) == 1 and value.stride(-1) == 1, "key/value: last dim must be contiguous")
+    _require(key.stride(1) == head_dim and value.stride(1) == head_dim, "key/value: heads must be head_dim apart")
+    _require(k_cache.stride(1) == D and v_cache.stride(1) == D, "caches: slot rows must be num_kv_heads*head_dim apart")
+    _require(slot_mapping.numel() == N, "slot_mapping must hold one slot per token")
+    if N == 0:
+        return
+    dev = _check_cuda(key, value, k_cache, v_cache, slot_mapping)
+    if key.dtype != k_cache.dtype or value.dtype != v_cache.dtype or key.element_size() != 2:
+        raise TypeError(f"store_kvcache: 16-bit key/value matching the cache dtype, got {key.dtype}/{k_cache.dtype}")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("store_kvcache: caches must be contiguous [num_blocks, block_size, HK, head_dim]")
+    slots = _as_i32(slot_mapping.reshape(-1), "slot_mapping")
+    lib = _lib.load()
+    _lib.check(lib.vox_store_kvcache(key.data_ptr(), value.data_ptr(), key.stride(0), value.stride(0),
+                                     k_cache.data_ptr(), v_cache.data_ptr(), k_cache.numel() // D, slots.data_ptr(),
+                                     N, num_heads, head_dim, _lib.stream_handle(dev)),
+               "store_kvcache")
+
+
+# --------------------------------------------------------------------------------------------------------------------
+# Decode
+
+
+def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, context_lens: torch.Tensor,
+                     block_tables: torch.Tensor, softmax_scale: float, out: torch.Tensor | None = None
+                     ) -> torch.Tensor:
+    """One query token per sequence: q [B, H, 128] (sequence rows may be strided) over the paged cache
+    [num_blocks, block_size, HK, 128] through block_tables int32 [B, max_blocks]; context_lens int32 [B].
+    Returns o [B, H, 128] bf16 (contiguous). Rows with context_lens == 0 get zeros."""
+    B, H, D = q.shape
+    dev = _check_cuda(q, k_cache, v_cache, context_lens, block_tables)
+    if q.dtype != torch.bfloat16 or k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
+        raise TypeError("decode attention takes bf16 q and caches")
+    if D != HEAD_DIM or q.stride(2) != 1 or q.stride(1) != D:
+        raise ValueError(f"q must be [B, H, {HEAD_DIM}] with contiguous heads, got {tuple(q.shape)} {q.stride()}")
+    if k_cache.dim() != 4 or not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("caches must be contiguous [num_blocks, block_size, HK, head_dim]")
+    if k_cache.shape != v_cache.shape:
+        raise ValueError("k_cache and v_cache shapes differ")
+    num_blocks, block_size, HK, Dk = k_cache.shape
+    if Dk != D:
+        raise ValueError("cache head_dim differs from q's")
+    if H % HK or H > MAX_DECODE_HEADS or HK not in (1, 2):
+        raise ValueError(f"decode supports H <= {MAX_DECODE_HEADS} query heads over 1 or 2 KV heads, got {H}/{HK}")
+    if context_lens.numel() != B or block_tables.dim() != 2 or block_tables.shape[0] < B:
+        raise ValueError("context_lens must be [B] and block_tables [B, max_blocks]")
+    if out is None:
+        out = torch.empty(B, H, D, dtype=q.dtype, device=dev)
+    if B == 0:
+        return out
+    if q.stride(0) == 0:
+        q = q.contiguous()
+    bt = block_tables if (block_tables.dtype == torch.int32 and block_tables.stride(1) == 1) else \
+        _as_i32(block_tables, "block_tables")
+    lens = _as_i32(context_lens.reshape(-1), "context_lens")
+    max_blocks = bt.shape[1]
+    lib = _lib.load()
+    ws_bytes = lib.vox_decode_workspace_bytes(B, max_blocks, block_size)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    counters = decode_counters(dev)
+    if B > counters.numel():
+        raise ValueError(f"decode batch {B} exceeds the {counters.numel()} arrival counters")
+    _lib.check(lib.vox_decode_attn(q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), num_blocks,
+                                   block_size, bt.data_ptr(), bt.stride(0), max_blocks, lens.data_ptr(), B, H, HK, D,
+                                   float(softmax_scale), ws.data_ptr(), ws.numel(), counters.data_ptr(),
+                                   counters.numel(), out.data_ptr(), _lib.stream_handle(dev)),
+               "decode_attn")
+    return out
+
+
+# --------------------------------------------------------------------------------------------------------------------
+# Prefill / varlen
+
+
+def varlen_attention(q: torch.Tensor, k: torch.Tensor | None, v: torch.Tensor | None, *,
+                     cu_seqlens_q: torch.Tensor | None, cu_seqlens_k: torch.Tensor | None, max_seqlen_q: int,
+                     softmax_scale: float, causal: bool, block_table: torch.Tensor | None = None,
+                     k_cache: torch.Tensor | None = None, v_cache: torch.Tensor | None = None,
+                     batch: int | None = None, uniform_seqlen_q: int = 0, uniform_seqlen_k: int = 0,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """The varlen prefill kernel. q [T, H, 128] (token rows may be strided). K/V from packed rows k / v
+    [Tk, HK, 128] or, with block_table, from k_cache / v_cache [num_blocks, block_size, HK, 128]. Sequences from
+    cu_seqlens_q / cu_seqlens_k (int32 [B + 1]) or, when both are None, `batch` sequences of uniform lengths.
+    Returns o [T, H, 128] bf16."""
+    T, H, D = q.shape
+    dev = _check_cuda(q)
+    if q.dtype != torch.bfloat16:
+        raise TypeError("varlen attention takes bf16 q")
+    if D != HEAD_DIM or q.stride(2) != 1 or q.stride(1) != D:
+        raise ValueError(f"q must be [T, H, {HEAD_DIM}] with contiguous heads, got {tuple(q.shape)} {q.stride()}")
+    if out is None:
+        out = torch.empty(T, H, D, dtype=q.dtype, device=dev)
+    if cu_seqlens_q is not None:
+        B = cu_seqlens_q.numel() - 1
+        if cu_seqlens_k is None or cu_seqlens_k.numel() != B + 1:
+            raise ValueError("cu_seqlens_k must have as many entries as cu_seqlens_q")
+        cu_q = _as_i32(cu_seqlens_q, "cu_seqlens_q")
+        cu_k = _as_i32(cu_seqlens_k, "cu_seqlens_k")
+        _check_cuda(q, cu_q, cu_k)
+    else:
+        B = int(batch or 0)
+        cu_q = cu_k = None
+    if T == 0 or B <= 0 or max_seqlen_q <= 0:
+        return out
+    lib = _lib.load()
+    if block_table is not None:
+        if k_cache is None or v_cache is None:
+            raise ValueError("block_table given without caches")
+        _check_cuda(q, k_cache, v_cache, block_table)
+        if k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
+            raise TypeError("caches must be bf16")
+        if k_cache.dim() != 4 or not (k_cache.is_contiguous() and v_cache.is_contiguous()) \
+                or k_cache.shape != v_cache.shape or k_cache.shape[3] != D:
+            raise ValueError("caches must be contiguous [num_blocks, block_size, HK, head_dim]")
+        num_blocks, block_size, HK, _ = k_cache.shape
+        bt = block_table if (block_table.dtype == torch.int32 and block_table.stride(1) == 1) else \
+            _as_i32(block_table, "block_table")
+        if bt.dim() != 2 or bt.shape[0] < B:
+            raise ValueError("block_table must be [B, max_blocks]")
+        args = (0, 0, 0, 0, k_cache.data_ptr(), v_cache.data_ptr(), num_blocks, block_size, bt.data_ptr(),
+                bt.stride(0), bt.shape[1])
+    else:
+        if k is None or v is None:
+            raise ValueError("packed K/V required without a block table")
+        _check_cuda(q, k, v)
+        if k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+            raise TypeError("k/v must be bf16")
+        HK = k.shape[1]
+        if k.dim() != 3 or k.shape[2] != D or k.stride(2) != 1 or k.stride(1) != D or v.shape != k.shape \
+                or v.stride(2) != 1 or v.stride(1) != D:
+            raise ValueError("k/v must be [Tk, HK, head_dim] with contiguous heads")
+        args = (k.data_ptr(), v.data_ptr(), k.stride(0), v.stride(0), 0, 0, 0, 0, 0, 0, 0)
+    if H % HK:
+        raise ValueError(f"num_heads {H} is not a multiple of num_kv_heads {HK}")
+    _lib.check(lib.vox_prefill_attn(q.data_ptr(), q.stride(0), *args,
+                                    None if cu_q is None else cu_q.data_ptr(),
+                                    None if cu_k is None else cu_k.data_ptr(), B, int(max_seqlen_q),
+                                    int(uniform_seqlen_q), int(uniform_seqlen_k), H, HK, D, float(softmax_scale),
+                                    1 if causal else 0, out.data_ptr(), out.stride(0), _lib.stream_handle(dev)),
+               "prefill_attn")
+    return out
+
+
+# --------------------------------------------------------------------------------------------------------------------
+# The flash-attn entry points the reference's Attention.forward calls
+
+
+def flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q, max_seqlen_k, cu_seqlens_k, softmax_scale=None,
+                           causal=False, block_table=None):
+    """q [T, H, D]; k / v packed [Tk, HK, D], or the paged caches [num_blocks, block_size, HK, D] with
+    block_table [B, max_blocks]. Returns o [T, H, D]. (Reference call: nanovllm_voxcpm/model/layers.py:337-348.)"""
+    scale = q.shape[-1] ** -0.5 if softmax_scale is None else softmax_scale
+    if block_table is not None:
+        return varlen_attention(q, None, None, cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_seqlens_k,
+                                max_seqlen_q=max_seqlen_q, softmax_scale=scale, causal=causal,
+                                block_table=block_table, k_cache=k, v_cache=v)
+    return varlen_attention(q, k, v, cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_seqlens_k, max_seqlen_q=max_seqlen_q,
+                            softmax_scale=scale, causal=causal)
+
+
+def flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=None, block_table=None, softmax_scale=None,
+                            causal=False):
+    """q [B, Lq, H, D] over the paged caches; cache_seqlens int32 [B] counts every key (cached + new); returns
+    o [B, Lq, H, D]. Lq == 1 (the engine's decode) runs the split-KV decode kernel; Lq > 1 runs the varlen kernel
+    with bottom-right causal alignment. (Reference call: nanovllm_voxcpm/model/layers.py:350-358.)"""
+    if block_table is None or cache_seqlens is None:
+        raise NotImplementedError("flash_attn_with_kvcache: the paged form (block_table, cache_seqlens) is supported")
+    B, Lq, H, D = q.shape
+    scale = D ** -0.5 if softmax_scale is None else softmax_scale
+    if Lq == 1:
+        return decode_attention(q[:, 0], k_cache, v_cache, cache_seqlens, block_table, scale).unsqueeze(1)
+    lens = _as_i32(cache_seqlens.reshape(-1), "cache_seqlens")
+    cu_q = torch.arange(0, (B + 1) * Lq, Lq, dtype=torch.int32, device=q.device)
+    cu_k = torch.zeros(B + 1, dtype=torch.int32, device=q.device)
+    torch.cumsum(lens, 0, out=cu_k[1:])
+    q3 = q.reshape(B * Lq, H, D)
+    o = varlen_attention(q3, None, None, cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, max_seqlen_q=Lq,
+                         softmax_scale=scale, causal=causal, block_table=block_table, k_cache=k_cache,
+                         v_cache=v_cache)
+    return o.view(B, Lq, H, D)
+
+
+def _token_rows(x: torch.Tensor) -> torch.Tensor:
+    """[B, L, heads, D] as [B*L, heads, D] token rows without a copy when rows are uniformly strided."""
+    B, L, Hx, D = x.shape
+    row = x.stride(1) if L > 1 else x.stride(0)
+    if B > 1 and x.stride(0) != L * row:
+        x = x.contiguous()
+        row = Hx * D
+    return x.as_strided((B * L, Hx, D), (row, x.stride(2), x.stride(3)))
+
+
+def flash_attn_func(q, k, v, softmax_scale=None, causal=False):
+    """Dense attention q [B, L, H, D], k / v [B, Lk, HK, D] (the non-causal branch of Attention.forward: LocEnc and
+    LocDiT rows). Returns o [B, L, H, D]. (Reference call: nanovllm_voxcpm/model/layers.py:359-361.)"""
+    B, L, H, D = q.shape
+    Lk = k.shape[1]
+    scale = D ** -0.5 if softmax_scale is None else softmax_scale
+    o = varlen_attention(_token_rows(q), _token_rows(k), _token_rows(v), cu_seqlens_q=None, cu_seqlens_k=None,
+                         max_seqlen_q=L, softmax_scale=scale, causal=causal, batch=B, uniform_seqlen_q=L,
+                         uniform_seqlen_k=Lk)
+    return o.view(B, L, H, D)
