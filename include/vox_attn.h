@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define VOX_ABI_VERSION 1
+#define VOX_ABI_VERSION 2
 
 #define VOX_OK 0
 #define VOX_EINVAL 1 /* bad argument: shape, stride, alignment or null pointer (reference: the asserts of
@@ -45,22 +45,21 @@ int vox_store_kvcache(const void* key, const void* value, int64_t key_row_stride
  *   k/v_cache    bf16 [num_blocks, block_size, num_kv_heads, head_dim], contiguous
  *   block_tables int32 [batch, bt_stride]; columns >= ceil(context_lens[b] / block_size) are never read
  *   context_lens int32 [batch]; 0 = padded row, whose output is written as zeros
- *   workspace    >= vox_decode_workspace_bytes(batch, max_blocks, block_size) bytes, contents scratch
- *   counters     int32 [num_counters >= batch], all zero on entry; the call leaves them zero again. Calls that
- *                share counters must be ordered on one stream.
+ *   workspace    >= vox_decode_workspace_bytes(batch, max_blocks, block_size) bytes of scratch (split-KV partials),
+ *                used by the two kernels the call launches in order on `stream`
  *   out          bf16 [batch, num_heads, head_dim], contiguous
  * Supported: head_dim 128, num_kv_heads 1 or 2, num_heads <= 16, block_size a multiple of 32. */
 int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
                     int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
                     int max_blocks, const int32_t* context_lens, int batch, int num_heads, int num_kv_heads,
-                    int head_dim, float softmax_scale, void* workspace, size_t workspace_bytes, int32_t* counters,
-                    int64_t num_counters, void* out, void* stream);
+                    int head_dim, float softmax_scale, void* workspace, size_t workspace_bytes, void* out,
+                    void* stream);
 
 /* Scratch bytes vox_decode_attn needs for a launch of this shape (split-KV partials). No reference counterpart:
  * flash-attn sizes its split-KV buffers internally (reference call site: nanovllm_voxcpm/model/layers.py:350). */
 size_t vox_decode_workspace_bytes(int batch, int max_blocks, int block_size);
 
-/* Tokens per decode workgroup for this shape (a multiple of 128), and a process-wide override for tuning
+/* Tokens per decode workgroup for this shape (a multiple of 64), and a process-wide override for tuning
  * (0 restores the built-in choice). No reference counterpart. */
 int vox_decode_chunk_tokens(int batch, int max_blocks, int block_size);
 void vox_set_decode_chunk_tokens(int tokens);

@@ -29,8 +29,10 @@ def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, scal
 
 def gather_pages(cache: torch.Tensor, table, n: int) -> torch.Tensor:
     """The first n tokens of one sequence's K or V through its block table: cache [pages, page, HK, D].
-    Reference: tests/test_kernel_references.py:199-201 (``k_cache[pages].reshape(-1, HK, D)[:n_k]``)."""
-    pages = torch.as_tensor(table, dtype=torch.long)
+    Reference: tests/test_kernel_references.py:199-201 (``k_cache[pages].reshape(-1, HK, D)[:n_k]``); only the
+    ceil(n / page) pages those tokens occupy are read, so padded or stale table columns are never touched."""
+    page = cache.shape[1]
+    pages = torch.as_tensor(table, dtype=torch.long)[:(n + page - 1) // page]
     HK, D = cache.shape[2], cache.shape[3]
     return cache[pages].reshape(-1, HK, D)[:n]
 

@@ -57,7 +57,7 @@ def test_store_rejects_bad_arguments_without_launching():
 def _decode(**over):
     p = ctypes.c_void_p(256)
     a = dict(q=p, qs=16 * 128, kc=p, vc=p, nb=4, bs=256, bt=p, bts=8, mb=8, lens=p, b=2, h=16, hk=2, d=128,
-             scale=0.088, ws=p, wsb=1 << 30, cnt=p, ncnt=16, out=p, stream=None)
+             scale=0.088, ws=p, wsb=1 << 30, out=p, stream=None)
     a.update(over)
     return _lib.load().vox_decode_attn(*a.values())
 
@@ -65,7 +65,7 @@ def _decode(**over):
 def test_decode_rejects_unsupported_shapes():
     assert _decode(b=0) == _lib.VOX_OK
     for over, msg in [(dict(d=64), "head_dim"), (dict(hk=4, h=16), "num_kv_heads"), (dict(h=32), "num_heads"),
-                      (dict(bs=100), "block_size"), (dict(bts=4), "block table"), (dict(ncnt=1), "counters"),
+                      (dict(bs=100), "block_size"), (dict(bts=4), "block table"),
                       (dict(wsb=10), "workspace"), (dict(qs=100), "row stride"), (dict(lens=None), "null"),
                       (dict(scale=float("nan")), "finite")]:
         assert _decode(**over) == _lib.VOX_EINVAL, over
@@ -77,15 +77,17 @@ def test_decode_workspace_and_chunk_choice():
     assert lib.vox_decode_workspace_bytes(0, 8, 256) == 0
     for b, mb in [(1, 2), (40, 6), (150, 8), (512, 4)]:
         chunk = lib.vox_decode_chunk_tokens(b, mb, 256)
-        assert chunk % 128 == 0 and 128 <= chunk <= 256
+        assert chunk % 64 == 0 and 64 <= chunk <= 1024
         chunks = -(-mb * 256 // chunk)
         assert lib.vox_decode_workspace_bytes(b, mb, 256) == b * chunks * (16 * 128 + 32) * 4
+    default = lib.vox_decode_chunk_tokens(150, 8, 256)
     lib.vox_set_decode_chunk_tokens(512)
     try:
         assert lib.vox_decode_chunk_tokens(150, 8, 256) == 512
+        assert lib.vox_decode_workspace_bytes(150, 8, 256) == 150 * 4 * (16 * 128 + 32) * 4
     finally:
         lib.vox_set_decode_chunk_tokens(0)
-    assert lib.vox_decode_chunk_tokens(150, 8, 256) == 128
+    assert lib.vox_decode_chunk_tokens(150, 8, 256) == default
 
 
 def test_prefill_rejects_bad_arguments():

@@ -98,15 +98,13 @@ def test_decode_chunk_sizes_agree(chunk):
         lib.vox_set_decode_chunk_tokens(0)
 
 
-def test_decode_counters_are_left_zero_across_calls():
-    from voxcpm2_arabic_dialects_turbo_amd.ops import decode_counters
-
+def test_decode_repeated_calls_of_changing_batch():
+    """Back-to-back calls that reuse the workspace with different batch sizes and split counts."""
     gen = torch.Generator().manual_seed(36)
     for n in (30, 7, 30, 64):
         lens = uniform_lens(gen, n, 100, 2048)
         kc, vc, tables = paged_pool(gen, lens, 8 * n)
         _check(randn(gen, n, H, D), kc, vc, lens, tables, f"batch {n}")
-        assert int(decode_counters(torch.device(DEV)).abs().sum()) == 0
 
 
 def test_decode_config4_layer_full_size():

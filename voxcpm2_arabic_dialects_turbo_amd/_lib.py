@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must be loaded before the library: shared HIP runti
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvoxattn.so")
 
 VOX_OK, VOX_EINVAL, VOX_EHIP = 0, 1, 2
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # every symbol include/vox_attn.h declares
 EXPORTS = (
@@ -39,8 +39,7 @@ _SIGNATURES = {
     "vox_store_kvcache": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _i64,
                                  _i32, _i32, _c_void_p]),
     "vox_decode_attn": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _i64, _i32,
-                               _c_void_p, _i32, _i32, _i32, _i32, _f32, _c_void_p, _size, _c_void_p, _i64,
-                               _c_void_p, _c_void_p]),
+                               _c_void_p, _i32, _i32, _i32, _i32, _f32, _c_void_p, _size, _c_void_p, _c_void_p]),
     "vox_decode_workspace_bytes": (_size, [_i32, _i32, _i32]),
     "vox_decode_chunk_tokens": (_i32, [_i32, _i32, _i32]),
     "vox_set_decode_chunk_tokens": (None, [_i32]),

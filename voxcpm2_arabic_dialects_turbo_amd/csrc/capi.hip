@@ -81,11 +81,11 @@ size_t vox_decode_workspace_bytes(int batch, int max_blocks, int block_size) {
 int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
                     int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
                     int max_blocks, const int32_t* context_lens, int batch, int num_heads, int num_kv_heads,
-                    int head_dim, float softmax_scale, void* workspace, size_t workspace_bytes, int32_t* counters,
-                    int64_t num_counters, void* out, void* stream) {
+                    int head_dim, float softmax_scale, void* workspace, size_t workspace_bytes, void* out,
+                    void* stream) {
   if (batch < 0) return fail(VOX_EINVAL, "decode_attn: batch < 0");
   if (batch == 0) return VOX_OK;
-  if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out || !counters)
+  if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out)
     return fail(VOX_EINVAL, "decode_attn: null pointer argument");
   if (head_dim != kHeadDim) return fail(VOX_EINVAL, "decode_attn: head_dim %d unsupported (128 only)", head_dim);
   if (num_kv_heads != 1 && num_kv_heads != 2)
@@ -100,14 +100,12 @@ int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, co
     return fail(VOX_EINVAL, "decode_attn: q row stride %lld", (long long)q_row_stride);
   if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out) || !aligned16(workspace))
     return fail(VOX_EINVAL, "decode_attn: q, caches, out and workspace must be 16-byte aligned");
-  if (num_counters < batch) return fail(VOX_EINVAL, "decode_attn: %lld counters for batch %d",
-                                        (long long)num_counters, batch);
   if (!std::isfinite(softmax_scale)) return fail(VOX_EINVAL, "decode_attn: softmax_scale is not finite");
   const size_t need = vox_decode_workspace_bytes(batch, max_blocks, block_size);
   if (workspace_bytes < need || (need && !workspace))
     return fail(VOX_EINVAL, "decode_attn: workspace of %zu bytes, %zu needed", workspace_bytes, need);
   const int chunk = vox_decode_chunk_tokens(batch, max_blocks, block_size);
-  if (chunk <= 0 || chunk % 128) return fail(VOX_EINVAL, "decode_attn: chunk %d not a multiple of 128", chunk);
+  if (chunk <= 0 || chunk % 64) return fail(VOX_EINVAL, "decode_attn: chunk %d not a multiple of 64", chunk);
   const int max_ctx = max_blocks * block_size;
 
   vox::DecodeArgs a;
@@ -128,7 +126,6 @@ int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, co
   a.chunk = chunk;
   a.max_chunks = (max_ctx + chunk - 1) / chunk;
   a.partials = (float*)workspace;
-  a.counters = counters;
   a.out = (uint16_t*)out;
   return hip_status(vox::launch_decode(a, num_kv_heads, max_ctx, (hipStream_t)stream), "decode_attn launch");
 }

@@ -11,12 +11,15 @@
 //    c = (kv head, d) with a block-diagonal query operand B[c, h] = q[h, d] if c's kv head is h's group else 0:
 //    the 16 MFMA columns are 16 real heads instead of 8 heads padded to 16, and each K slot row feeds the MFMA A
 //    operand straight from global memory (lane = token, 16 contiguous bytes per k-step).
-//  * Each wave walks 32-token tiles: S^T[32 tok x 16 heads] = K Q^T (2 x HK*4 MFMAs 16x16x32), online softmax in
-//    fp32 with exp2, then O^T[d, h] += V^T P^T. V needs its token axis contiguous per lane, so each wave transposes
-//    its V tile through a private LDS buffer; P^T is already in the MFMA B layout (no shuffles).
+//  * Each wave walks 16-token tiles (K loaded into registers in MFMA layout, V coalesced; three waves per SIMD
+//    keep loads in flight): S^T[16 tok x 16 heads] = K Q^T (HK*4 MFMA 16x16x32), online softmax in fp32 with exp2, then
+//    O^T[c, h] += V^T P^T (MFMA 16x16x16 per 16 output dims and kv head). V is written row-major into a private LDS
+//    tile with 16-byte stores and read back transposed by ds_read_b64_tr_b16, which hands each lane four tokens of
+//    one column: exactly the A operand. P^T is already in the B layout, no shuffles.
 //  * Split-KV: chunks of a sequence run as independent workgroups. The four waves of a workgroup are merged in LDS;
-//    chunks are merged by the last workgroup of the sequence to finish (atomic arrival counter, reset to zero by
-//    that workgroup), so one launch per layer does the whole decode with no combine kernel.
+//    a sequence that fits one chunk is written directly, the others leave fp32 partials (O, m, l) that a small
+//    second kernel merges. Merging in the split kernel itself (last workgroup to arrive) was measured slower: every
+//    workgroup then holds its CU slot through a write-through wait and an atomic round trip.
 #include "vox_common.h"
 #include "vox_kernels.h"
 
@@ -25,31 +28,94 @@ namespace vox {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kTile = 32;     // tokens per wave iteration
+constexpr int kTile = 16;     // tokens per wave iteration
 constexpr int kWaves = 4;
-constexpr int kVtStride = 36; // bf16 per LDS row of a transposed V tile (32 tokens + 4 pad)
 constexpr int kMaxHeads = 16;
 
-template <int HK>
-__global__ __launch_bounds__(256, 2) void decode_kernel(DecodeArgs p) {
-  constexpr int ROW = HK * kD;   // elements per cache slot row
-  constexpr int KC = ROW / 32;   // MFMA k-steps per score tile
-  // Per-wave transposed V tiles; reused as fp32 scratch for the in-workgroup merge.
-  __shared__ __attribute__((aligned(16))) uint16_t vt[kWaves][ROW][kVtStride];
-  __shared__ int last_flag;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-  const int b = blockIdx.y;
-  const int c = blockIdx.x;
+__device__ __forceinline__ f32x4 mfma_16x16x16(s16x4 a, s16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+// Transposed LDS read: within each 16-lane group, lane j returns element j%4 of the 8-byte chunks that lanes
+// 4r + j/4 (r = 0..3) address, i.e. four rows of one column when lanes 4r + q point at row r, column 4q.
+__device__ __forceinline__ s16x4 lds_read_tr16(const uint16_t* p) {
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+}
+
+template <int HK>
+struct Tile {
+  static constexpr int ROW = HK * kD;              // elements per cache slot row
+  static constexpr int KC = ROW / 32;              // score MFMA k-steps
+  static constexpr int VP = kTile * ROW / 8 / 64;  // 16-byte V pieces per lane per tile
+  static constexpr int PPR = ROW / 8;              // 16-byte pieces per slot row
+  u32x4 k[KC];
+  u32x4 v[VP];
+  bool ok;  // the tile's cache block is mapped
+};
+
+// Issues the loads of the 16-token tile whose first token sits at cache slot slot0 (a tile never straddles a cache
+// block). Every load is unconditional and in bounds, so the compiler can count outstanding loads exactly: the caller
+// maps an unmapped block to block 0 and masks what it read. K rows land in MFMA A layout (lane = token r16), V
+// pieces coalesced (16 bytes per lane, whole slot rows per instruction).
+template <int HK>
+__device__ __forceinline__ void load_tile(Tile<HK>& T, const DecodeArgs& p, int64_t slot0, int r16, int jq,
+                                          int lane) {
+  using TT = Tile<HK>;
+  const uint16_t* kp = p.k_cache + (slot0 + r16) * TT::ROW + jq * 8;
+#pragma unroll
+  for (int kc = 0; kc < TT::KC; ++kc) T.k[kc] = ld_g16(kp + kc * 32);
+#pragma unroll
+  for (int i = 0; i < TT::VP; ++i) {
+    const int pc = i * 64 + lane;
+    T.v[i] = ld_g16(p.v_cache + (slot0 + pc / TT::PPR) * TT::ROW + (pc % TT::PPR) * 8);
+  }
+}
+
+template <int HK>
+__global__ __launch_bounds__(256, 3) void decode_kernel(DecodeArgs p) {
+  using TT = Tile<HK>;
+  constexpr int ROW = TT::ROW;
+  constexpr int VROW = ROW + 16;  // padded LDS row: the 16 rows a transposed read touches hit distinct banks
+  // Per-wave V tiles [16 tokens][VROW]; reused as fp32 scratch for the in-workgroup merge.
+  constexpr int kVtElems = kWaves * kTile * VROW;
+  constexpr int kRedFloats = kWaves * kMaxHeads * kD + 2 * kWaves * kMaxHeads;
+  constexpr int kLdsBytes = (kVtElems * 2 > kRedFloats * 4) ? kVtElems * 2 : kRedFloats * 4;
+  __shared__ __attribute__((aligned(16))) unsigned char lds_raw[kLdsBytes];
+
+  // Sequences vary fastest in dispatch order: chunk 0 of every sequence first, so the trailing chunk ids that most
+  // sequences do not have (early exits) are dispatched last instead of between live workgroups.
+  const int b = blockIdx.x;
+  const int c = blockIdx.y;
   const int tid = threadIdx.x;
   const int w = tid >> 6;
   const int lane = tid & 63;
   const int r16 = lane & 15;
   const int jq = lane >> 4;
   const int H = p.num_heads;
-  // A context longer than the block table can address is cut to it: keeps chunk ids inside the partial buffer.
-  const int ctx = min(p.context_lens[b], p.max_blocks * p.block_size);
-  uint16_t* out_b = p.out + (int64_t)b * H * kD;
+  const int max_ctx = p.max_blocks * p.block_size;
+  const int tok0 = c * p.chunk;  // < max_ctx: c < max_chunks
+  const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
 
+  // Independent loads issued together (one round trip): the context length, this lane's query row and the block
+  // id of this wave's first tile. Query row of head r16: d = kq*32 + jq*8 + [0, 8); the score B operand for k-step
+  // kc is piece kc % 4 when kc's kv head (kc / 4) is the lane's group, else zero: block-diagonal over (kv head, d).
+  const int ctx_raw = p.context_lens[b];
+  const int h = r16;
+  const int hg = h < H ? h / p.group : -1;
+  u32x4 qv[4];
+  {
+    const uint16_t* qb = p.q + (int64_t)b * p.q_row_stride + (int64_t)(h < H ? h : 0) * kD + jq * 8;
+#pragma unroll
+    for (int kq = 0; kq < 4; ++kq) qv[kq] = ld_g16(qb + kq * 32);
+  }
+  int64_t blk = bt_row[min(tok0 + w * kTile, max_ctx - 1) / p.block_size];
+
+  // A context longer than the block table can address is cut to it: keeps chunk ids inside the partial buffer.
+  const int ctx = min(ctx_raw, max_ctx);
+  uint16_t* out_b = p.out + (int64_t)b * H * kD;
   if (ctx <= 0) {  // padded row of a captured batch: defined zeros
     if (c == 0)
       for (int i = tid; i < H * kD; i += 256) out_b[i] = 0;
@@ -57,18 +123,7 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(DecodeArgs p) {
   }
   const int n_chunks = (ctx + p.chunk - 1) / p.chunk;
   if (c >= n_chunks) return;
-  const int tok0 = c * p.chunk;
   const int tok_end = min(ctx, tok0 + p.chunk);
-
-  // Block-diagonal query operand, lane (head r16, k-group jq): c = kc*32 + jq*8 + [0, 8).
-  const int h = r16;
-  const int hg = h < H ? h / p.group : -1;
-  u32x4 qop[KC];
-  {
-    const uint16_t* qb = p.q + (int64_t)b * p.q_row_stride + (int64_t)h * kD + jq * 8;
-#pragma unroll
-    for (int kc = 0; kc < KC; ++kc) qop[kc] = (hg == kc / 4) ? ld_g16(qb + (kc % 4) * 32) : zero4();
-  }
 
   float m = -INFINITY;
   float lsum = 0.f;
@@ -76,102 +131,84 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(DecodeArgs p) {
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  uint16_t(*vtw)[kVtStride] = vt[w];
+  uint16_t* vt = reinterpret_cast<uint16_t*>(lds_raw) + w * kTile * VROW;
+  // this lane's transposed-read address inside a d-tile: row jq*4 + r16/4, column 4*(r16%4)
+  const uint16_t* vtr = vt + (jq * 4 + (r16 >> 2)) * VROW + 4 * (r16 & 3);
 
-  for (int t0 = tok0 + w * kTile; t0 < tok_end; t0 += kWaves * kTile) {
-    // A 32-token tile never straddles a cache block (block_size % 32 == 0, t0 % 32 == 0).
-    const int col = t0 / p.block_size;
-    const int64_t blk = col < p.max_blocks ? (int64_t)p.block_tables[(int64_t)b * p.bt_stride + col] : -1;
-    const bool blk_ok = blk >= 0 && blk < p.num_blocks;
-    const int64_t slot0 = blk * p.block_size + (t0 % p.block_size);
-
-    u32x4 kr[2][KC], vr[2][KC];
+  auto compute = [&](const Tile<HK>& T, int t0) {
+    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const bool ok = blk_ok && (t0 + s * 16 + r16) < tok_end;
-      const int64_t off = (slot0 + s * 16 + r16) * ROW + jq * 8;
-      const uint16_t* kp = p.k_cache + off;
-      const uint16_t* vp = p.v_cache + off;
-#pragma unroll
-      for (int kc = 0; kc < KC; ++kc) {
-        kr[s][kc] = ok ? ld_g16(kp + kc * 32) : zero4();
-        vr[s][kc] = ok ? ld_g16(vp + kc * 32) : zero4();
-      }
-    }
-
-    // S^T tile: lane (head r16) holds tokens t0 + s*16 + jq*4 + [0, 4).
-    f32x4 sacc[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      sacc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kc = 0; kc < KC; ++kc) sacc[s] = mfma_16x16x32(kr[s][kc], qop[kc], sacc[s]);
-    }
-
-    float x[2][4];
+    for (int kc = 0; kc < TT::KC; ++kc) s = mfma_16x16x32(T.k[kc], hg == kc / 4 ? qv[kc % 4] : zero4(), s);
+    // lane (head r16) holds tokens t0 + jq*4 + [0, 4)
+    float x[4];
     float tmax = -INFINITY;
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const bool ok = blk_ok && (t0 + s * 16 + jq * 4 + rr) < tok_end;
-        x[s][rr] = ok ? sacc[s][rr] * p.scale_log2 : -INFINITY;
-        tmax = fmaxf(tmax, x[s][rr]);
-      }
+    for (int rr = 0; rr < 4; ++rr) {
+      const bool ok = T.ok && (t0 + jq * 4 + rr) < tok_end;
+      x[rr] = ok ? s[rr] * p.scale_log2 : -INFINITY;
+      tmax = fmaxf(tmax, x[rr]);
+    }
     tmax = col_max4(tmax);
     const float m_new = fmaxf(m, tmax);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
     const float alpha = fast_exp2(m - m_use);
     float ps = 0.f;
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        x[s][rr] = fast_exp2(x[s][rr] - m_use);
-        ps += x[s][rr];
-      }
+    for (int rr = 0; rr < 4; ++rr) {
+      x[rr] = fast_exp2(x[rr] - m_use);
+      ps += x[rr];
+    }
     lsum = lsum * alpha + ps;
     m = m_new;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
 
-    // V tile -> LDS, transposed to [c][token].
+    // V tile -> LDS, row-major, 16-byte stores; rows of tokens past tok_end or of an unmapped block are zeroed
+    // (they meet p = 0 in P V, and unwritten cache slots may hold any bit pattern)
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int kc = 0; kc < KC; ++kc) {
-        const u32x4 vv = vr[s][kc];
-        const int row = kc * 32 + jq * 8;
-        const int tc = s * 16 + r16;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          vtw[row + 2 * e][tc] = (uint16_t)(vv[e] & 0xffffu);
-          vtw[row + 2 * e + 1][tc] = (uint16_t)(vv[e] >> 16);
-        }
-      }
-    wave_lds_sync();
-
-    // P^T operand: k-slots jq*8 + [0,4) = tokens jq*4 + [0,4), jq*8 + [4,8) = tokens 16 + jq*4 + [0,4).
-    const u32x4 pv = u32x4{pack_bf16x2(x[0][0], x[0][1]), pack_bf16x2(x[0][2], x[0][3]),
-                           pack_bf16x2(x[1][0], x[1][1]), pack_bf16x2(x[1][2], x[1][3])};
-#pragma unroll
-    for (int g = 0; g < HK; ++g) {
-      const u32x4 pb = (hg == g) ? pv : zero4();
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const uint16_t* row = vtw[g * kD + dt * 16 + r16];
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(row + jq * 4);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(row + 16 + jq * 4);
-        acc[dt] = mfma_16x16x32(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb, acc[dt]);
-      }
+    for (int i = 0; i < TT::VP; ++i) {
+      const int pc = i * 64 + lane;
+      const bool ok = T.ok && (t0 + pc / TT::PPR) < tok_end;
+      *reinterpret_cast<u32x4*>(vt + (pc / TT::PPR) * VROW + (pc % TT::PPR) * 8) = ok ? T.v[i] : zero4();
     }
     wave_lds_sync();
+
+    // P^T operand: k-slots jq*4 + [0, 4) = tokens jq*4 + [0, 4)
+    const uint32_t p01 = pack_bf16x2(x[0], x[1]);
+    const uint32_t p23 = pack_bf16x2(x[2], x[3]);
+    const s16x4 pv = __builtin_bit_cast(s16x4, u32x2{p01, p23});
+    const s16x4 pz = s16x4{0, 0, 0, 0};
+#pragma unroll
+    for (int g = 0; g < HK; ++g) {
+      const s16x4 pb = (hg == g) ? pv : pz;
+      s16x4 va[8];
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) va[dt] = lds_read_tr16(vtr + g * kD + dt * 16);
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) acc[dt] = mfma_16x16x16(va[dt], pb, acc[dt]);
+    }
+    wave_lds_sync();
+  };
+
+  // This wave's tiles: tok0 + w*16 + k*64. Latency is hidden across waves (3 per SIMD), not inside one; the next
+  // tile's block id is read one tile ahead so each tile costs one memory round trip. Columns stay below max_blocks
+  // because the context is cut to the table's reach.
+  const int step = kWaves * kTile;
+  for (int t0 = tok0 + w * kTile; t0 < tok_end; t0 += step) {
+    const int tn = min(t0 + step, tok_end - 1);
+    const int64_t blk_next = bt_row[tn / p.block_size];
+    Tile<HK> T;
+    T.ok = blk >= 0 && blk < p.num_blocks;
+    load_tile<HK>(T, p, (T.ok ? blk : 0) * p.block_size + (t0 % p.block_size), r16, jq, lane);
+    __builtin_amdgcn_sched_barrier(0);  // all of the tile's loads issue before any of them is waited on
+    compute(T, t0);
+    blk = blk_next;
   }
 
   // ---- merge the four waves of this workgroup (fp32, in LDS) ----
   lsum = col_sum4(lsum);
   __syncthreads();
-  float* red = reinterpret_cast<float*>(&vt[0][0][0]);
+  float* red = reinterpret_cast<float*>(lds_raw);
   constexpr int kMOff = kWaves * kMaxHeads * kD;
   constexpr int kLOff = kMOff + kWaves * kMaxHeads;
 #pragma unroll
@@ -212,7 +249,7 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(DecodeArgs p) {
     return;
   }
 
-  // ---- split-KV: publish this chunk's partial, the last chunk of the sequence to arrive merges them ----
+  // ---- split-KV: publish this chunk's partial; decode_merge_kernel (next on the stream) combines them ----
   float* part = p.partials + ((int64_t)b * p.max_chunks + c) * kPartialFloats;
   *reinterpret_cast<f32x4*>(&part[hh * kD + d0]) = f32x4{o[0], o[1], o[2], o[3]};
   *reinterpret_cast<f32x4*>(&part[hh * kD + d0 + 4]) = f32x4{o[4], o[5], o[6], o[7]};
@@ -220,57 +257,65 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(DecodeArgs p) {
     part[kMaxHeads * kD + hh] = M;
     part[kMaxHeads * kD + kMaxHeads + hh] = L;
   }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const int prev = atomicAdd(&p.counters[b], 1);
-    last_flag = (prev == n_chunks - 1);
-  }
-  __syncthreads();
-  if (!last_flag) return;
-  __threadfence();
+}
 
+// Combines the chunk partials of every sequence that the decode kernel split (n_chunks > 1): online rescale over
+// the chunks (fp32), normalize, bf16. One workgroup per sequence, thread = (head, 8 dims); partial loads of four
+// chunks are issued together. Runs after decode_kernel on the same stream, which makes the partials visible.
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs p) {
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int hh = tid >> 4;
+  const int d0 = (tid & 15) * 8;
+  const int ctx = min(p.context_lens[b], p.max_blocks * p.block_size);
+  const int n_chunks = (ctx + p.chunk - 1) / p.chunk;
+  if (n_chunks <= 1 || hh >= p.num_heads) return;
   const float* pb = p.partials + (int64_t)b * p.max_chunks * kPartialFloats;
-  float M2 = -INFINITY;
-  for (int cc = 0; cc < n_chunks; ++cc) M2 = fmaxf(M2, pb[cc * kPartialFloats + kMaxHeads * kD + hh]);
-  const float M2u = M2 == -INFINITY ? 0.f : M2;
-  float L2 = 0.f;
+  float M2 = -INFINITY, L2 = 0.f;
   float o2[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) o2[i] = 0.f;
-  for (int cc = 0; cc < n_chunks; ++cc) {
-    const float* pc = pb + cc * kPartialFloats;
-    const float e = fast_exp2(pc[kMaxHeads * kD + hh] - M2u);
-    L2 += e * pc[kMaxHeads * kD + kMaxHeads + hh];
-    const f32x4 a = *reinterpret_cast<const f32x4*>(&pc[hh * kD + d0]);
-    const f32x4 bq = *reinterpret_cast<const f32x4*>(&pc[hh * kD + d0 + 4]);
-    o2[0] += e * a[0];
-    o2[1] += e * a[1];
-    o2[2] += e * a[2];
-    o2[3] += e * a[3];
-    o2[4] += e * bq[0];
-    o2[5] += e * bq[1];
-    o2[6] += e * bq[2];
-    o2[7] += e * bq[3];
+  for (int c0 = 0; c0 < n_chunks; c0 += 4) {
+    float mc[4], lc[4];
+    f32x4 oa[4], ob[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float* pc = pb + (int64_t)min(c0 + u, n_chunks - 1) * kPartialFloats;
+      mc[u] = (c0 + u < n_chunks) ? pc[kMaxHeads * kD + hh] : -INFINITY;
+      lc[u] = pc[kMaxHeads * kD + kMaxHeads + hh];
+      oa[u] = *reinterpret_cast<const f32x4*>(&pc[hh * kD + d0]);
+      ob[u] = *reinterpret_cast<const f32x4*>(&pc[hh * kD + d0 + 4]);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float mn = fmaxf(M2, mc[u]);
+      const float mu = mn == -INFINITY ? 0.f : mn;
+      const float a = fast_exp2(M2 - mu);
+      const float e = fast_exp2(mc[u] - mu);
+      L2 = L2 * a + e * lc[u];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o2[i] = o2[i] * a + e * oa[u][i];
+        o2[i + 4] = o2[i + 4] * a + e * ob[u][i];
+      }
+      M2 = mn;
+    }
   }
-  if (hh < H) {
-    const float inv = L2 > 0.f ? 1.f / L2 : 0.f;
-    const u32x4 ov = u32x4{pack_bf16x2(o2[0] * inv, o2[1] * inv), pack_bf16x2(o2[2] * inv, o2[3] * inv),
-                           pack_bf16x2(o2[4] * inv, o2[5] * inv), pack_bf16x2(o2[6] * inv, o2[7] * inv)};
-    *reinterpret_cast<u32x4*>(out_b + hh * kD + d0) = ov;
-  }
-  if (tid == 0) atomicExch(&p.counters[b], 0);
+  const float inv = L2 > 0.f ? 1.f / L2 : 0.f;
+  const u32x4 ov = u32x4{pack_bf16x2(o2[0] * inv, o2[1] * inv), pack_bf16x2(o2[2] * inv, o2[3] * inv),
+                         pack_bf16x2(o2[4] * inv, o2[5] * inv), pack_bf16x2(o2[6] * inv, o2[7] * inv)};
+  *reinterpret_cast<u32x4*>(p.out + ((int64_t)b * p.num_heads + hh) * kD + d0) = ov;
 }
 
 }  // namespace
 
 int decode_chunk_tokens(int batch, int max_ctx) {
-  // Chunks are multiples of one 4-wave x 32-token step. Prefer 256-token chunks (fewer partials to merge), halve
-  // them while the grid would leave the 256 CUs with less than ~8 workgroups each.
+  // Chunks are multiples of one 4-wave x 16-token step. Prefer 256-token chunks (fewer partials to merge), halve
+  // them while the grid would leave the 256 CUs with less than ~4 workgroups each.
   int chunk = 256;
-  while (chunk > kWaves * kTile) {
+  while (chunk > kWaves * kTile * 2) {
     const int64_t wgs = (int64_t)batch * ((max_ctx + chunk - 1) / chunk);
-    if (wgs >= 2048) break;
+    if (wgs >= 1024) break;
     chunk /= 2;
   }
   return chunk;
@@ -278,11 +323,14 @@ int decode_chunk_tokens(int batch, int max_ctx) {
 
 hipError_t launch_decode(const DecodeArgs& a, int num_kv_heads, int max_ctx, hipStream_t stream) {
   const int n_chunks = (max_ctx + a.chunk - 1) / a.chunk;
-  dim3 grid((unsigned)(n_chunks > 0 ? n_chunks : 1), (unsigned)a.batch);
+  dim3 grid((unsigned)a.batch, (unsigned)(n_chunks > 0 ? n_chunks : 1));
   if (num_kv_heads == 1)
     decode_kernel<1><<<grid, dim3(256), 0, stream>>>(a);
   else
     decode_kernel<2><<<grid, dim3(256), 0, stream>>>(a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || n_chunks <= 1) return e;
+  decode_merge_kernel<<<dim3((unsigned)a.batch), dim3(256), 0, stream>>>(a);
   return hipGetLastError();
 }
 

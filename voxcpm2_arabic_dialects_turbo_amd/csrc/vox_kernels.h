@@ -24,10 +24,9 @@ struct DecodeArgs {
   int num_heads;
   int group;                  // H / HK
   float scale_log2;           // softmax_scale * log2(e)
-  int chunk;                  // tokens per workgroup (multiple of 128)
+  int chunk;                  // tokens per workgroup (multiple of 64)
   int max_chunks;             // ceil(max_blocks * block_size / chunk)
   float* partials;            // [B, max_chunks, kPartialFloats]
-  int32_t* counters;          // [B], zero on entry, zero again on exit
   uint16_t* out;              // bf16 [B, H, 128], contiguous
 };
 

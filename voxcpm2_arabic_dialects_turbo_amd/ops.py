@@ -12,18 +12,12 @@ int32 index tensors. Decode takes up to 16 query heads over 1 or 2 KV heads.
 
 from __future__ import annotations
 
-import threading
-
 import torch
 
 from . import _lib
 
 HEAD_DIM = 128
 MAX_DECODE_HEADS = 16
-DECODE_COUNTERS = 1 << 16  # arrival counters per device: the largest decode batch one launch may take
-
-_counters: dict[int, torch.Tensor] = {}
-_counters_lock = threading.Lock()
 
 
 def _require(cond: bool, msg: str) -> None:
@@ -45,28 +39,6 @@ def _as_i32(t: torch.Tensor, name: str) -> torch.Tensor:
     if t.dtype in (torch.int64, torch.int16, torch.uint8, torch.int8):
         return t.to(torch.int32).contiguous()
     raise TypeError(f"{name} must be an integer tensor, got {t.dtype}")
-
-
-def decode_counters(device: torch.device) -> torch.Tensor:
-    """The device's persistent int32 arrival counters of the split-KV decode (all zero between launches).
-
-    Created zero-filled on first use outside graph capture; every decode launch leaves them zero again. Launches on
-    one device that share them must be ordered on one stream (the reference runs each engine on one stream)."""
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    t = _counters.get(idx)
-    if t is not None:
-        return t
-    if torch.cuda.is_current_stream_capturing():
-        raise RuntimeError(
-            "decode_attn: its arrival counters must be created by an eager decode call before graph capture "
-            "(run the warm-up step first, or call ops.decode_counters(device) before capturing)"
-        )
-    with _counters_lock:
-        t = _counters.get(idx)
-        if t is None:
-            t = torch.zeros(DECODE_COUNTERS, dtype=torch.int32, device=torch.device("cuda", idx))
-            _counters[idx] = t
-    return t
 
 
 # --------------------------------------------------------------------------------------------------------------------
@@ -139,13 +111,10 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     lib = _lib.load()
     ws_bytes = lib.vox_decode_workspace_bytes(B, max_blocks, block_size)
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
-    counters = decode_counters(dev)
-    if B > counters.numel():
-        raise ValueError(f"decode batch {B} exceeds the {counters.numel()} arrival counters")
     _lib.check(lib.vox_decode_attn(q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), num_blocks,
                                    block_size, bt.data_ptr(), bt.stride(0), max_blocks, lens.data_ptr(), B, H, HK, D,
-                                   float(softmax_scale), ws.data_ptr(), ws.numel(), counters.data_ptr(),
-                                   counters.numel(), out.data_ptr(), _lib.stream_handle(dev)),
+                                   float(softmax_scale), ws.data_ptr(), ws.numel(), out.data_ptr(),
+                                   _lib.stream_handle(dev)),
                "decode_attn")
     return out
 
