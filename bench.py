@@ -43,6 +43,8 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
     p.add_argument("--decode-only", action="store_true", help="headline decode only (no prefill legs)")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="also run 5 device copies of 256 MiB: the reference a PMC byte counter is scaled by")
     return p.parse_args()
 
 
@@ -278,6 +280,13 @@ def main():
     from voxcpm2_arabic_dialects_turbo_amd import _lib
 
     _lib.load()
+    if args.calibrate_copy:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     res = bench_decode(args, dev)
     value = res["step_bytes"] / (res["ms_per_step"] * 1e-3) / 1e9
     achieved = res["launch_bytes"] / (res["launch_ms"] * 1e-3) / 1e9
@@ -306,7 +315,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_kernel<2>",
+            "kernel": "decode_kernel<2> + decode_merge_kernel (one decode call)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
