@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define VOX_ABI_VERSION 2
+#define VOX_ABI_VERSION 3
 
 #define VOX_OK 0
 #define VOX_EINVAL 1 /* bad argument: shape, stride, alignment or null pointer (reference: the asserts of
@@ -45,8 +45,8 @@ int vox_store_kvcache(const void* key, const void* value, int64_t key_row_stride
  *   k/v_cache    bf16 [num_blocks, block_size, num_kv_heads, head_dim], contiguous
  *   block_tables int32 [batch, bt_stride]; columns >= ceil(context_lens[b] / block_size) are never read
  *   context_lens int32 [batch]; 0 = padded row, whose output is written as zeros
- *   workspace    >= vox_decode_workspace_bytes(batch, max_blocks, block_size) bytes of scratch (split-KV partials),
- *                used by the two kernels the call launches in order on `stream`
+ *   workspace    >= vox_decode_workspace_bytes(batch) bytes of scratch (split-KV partials), used by the two
+ *                kernels the call launches in order on `stream`
  *   out          bf16 [batch, num_heads, head_dim], contiguous
  * Supported: head_dim 128, num_kv_heads 1 or 2, num_heads <= 16, block_size a multiple of 32. */
 int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
@@ -55,14 +55,14 @@ int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, co
                     int head_dim, float softmax_scale, void* workspace, size_t workspace_bytes, void* out,
                     void* stream);
 
-/* Scratch bytes vox_decode_attn needs for a launch of this shape (split-KV partials). No reference counterpart:
- * flash-attn sizes its split-KV buffers internally (reference call site: nanovllm_voxcpm/model/layers.py:350). */
-size_t vox_decode_workspace_bytes(int batch, int max_blocks, int block_size);
+/* Scratch bytes vox_decode_attn needs for `batch` sequences on the current device (split-KV partials). No reference
+ * counterpart: flash-attn sizes its split-KV buffers internally (reference call site: nanovllm_voxcpm/model/layers.py:350). */
+size_t vox_decode_workspace_bytes(int batch);
 
-/* Tokens per decode workgroup for this shape (a multiple of 64), and a process-wide override for tuning
- * (0 restores the built-in choice). No reference counterpart. */
-int vox_decode_chunk_tokens(int batch, int max_blocks, int block_size);
-void vox_set_decode_chunk_tokens(int tokens);
+/* Workgroups the decode split kernel runs on the current device (3 per CU), and a process-wide override for tuning
+ * and tests (0 restores the built-in choice). No reference counterpart. */
+int vox_decode_workgroups(void);
+void vox_set_decode_workgroups(int workgroups);
 
 /* Varlen attention for prefill steps. Replaces flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q,
  * max_seqlen_k, cu_seqlens_k, softmax_scale, causal=True, block_table) (reference: nanovllm_voxcpm/model/layers.py:

@@ -72,22 +72,24 @@ def test_decode_rejects_unsupported_shapes():
         assert msg in _err(), (over, _err())
 
 
-def test_decode_workspace_and_chunk_choice():
+def test_decode_workspace_and_grid_choice():
     lib = _lib.load()
-    assert lib.vox_decode_workspace_bytes(0, 8, 256) == 0
-    for b, mb in [(1, 2), (40, 6), (150, 8), (512, 4)]:
-        chunk = lib.vox_decode_chunk_tokens(b, mb, 256)
-        assert chunk % 64 == 0 and 64 <= chunk <= 1024
-        chunks = -(-mb * 256 // chunk)
-        assert lib.vox_decode_workspace_bytes(b, mb, 256) == b * chunks * (16 * 128 + 32) * 4
-    default = lib.vox_decode_chunk_tokens(150, 8, 256)
-    lib.vox_set_decode_chunk_tokens(512)
+    assert lib.vox_decode_workspace_bytes(0) == 0
+    grid = lib.vox_decode_workgroups()
+    assert grid > 0 and grid % 2 == 0  # 2 workgroups per CU (512 on an MI355X, also the fallback without a GPU)
+    def need(b, g):
+        up = lambda x: -(-x // 256) * 256
+        s = min(b, 512)  # sequences per launch
+        return up((s + g) * (16 * 128 + 32) * 4) + up((s + 1) * 4)
+    for b in (1, 40, 150, 512, 5000):
+        assert lib.vox_decode_workspace_bytes(b) == need(b, grid)
+    lib.vox_set_decode_workgroups(7)
     try:
-        assert lib.vox_decode_chunk_tokens(150, 8, 256) == 512
-        assert lib.vox_decode_workspace_bytes(150, 8, 256) == 150 * 4 * (16 * 128 + 32) * 4
+        assert lib.vox_decode_workgroups() == 7
+        assert lib.vox_decode_workspace_bytes(150) == need(150, 7)
     finally:
-        lib.vox_set_decode_chunk_tokens(0)
-    assert lib.vox_decode_chunk_tokens(150, 8, 256) == default
+        lib.vox_set_decode_workgroups(0)
+    assert lib.vox_decode_workgroups() == grid
 
 
 def test_prefill_rejects_bad_arguments():

@@ -85,17 +85,20 @@ def test_decode_strided_query_rows_and_small_blocks():
     attn_close(out, ref.decode(q.float().cpu(), kc, vc, lens, tables, SCALE), "strided q")
 
 
-@pytest.mark.parametrize("chunk", [128, 256, 512, 2048])
-def test_decode_chunk_sizes_agree(chunk):
+@pytest.mark.parametrize("grid", [1, 2, 7, 64, 333, 768, 4000])
+def test_decode_split_grids_agree(grid):
+    """The split kernel's range partition at many grid sizes: one workgroup holding every sequence, ranges cutting
+    sequences anywhere, more workgroups than steps (empty ranges)."""
     gen = torch.Generator().manual_seed(35)
-    lens = uniform_lens(gen, 20, 1, 2048)
-    kc, vc, tables = paged_pool(gen, lens, 200)
+    lens = uniform_lens(gen, 20, 1, 2048) + [0, 64, 65]
+    kc, vc, tables = paged_pool(gen, [max(n, 1) for n in lens], 200)
     lib = _lib.load()
-    lib.vox_set_decode_chunk_tokens(chunk)
+    lib.vox_set_decode_workgroups(grid)
     try:
-        _check(randn(gen, 20, H, D), kc, vc, lens, tables, f"chunk {chunk}")
+        (_, _), out = _check(randn(gen, len(lens), H, D), kc, vc, lens, tables, f"grid {grid}")
+        assert int(out[20].abs().sum()) == 0
     finally:
-        lib.vox_set_decode_chunk_tokens(0)
+        lib.vox_set_decode_workgroups(0)
 
 
 def test_decode_repeated_calls_of_changing_batch():
@@ -105,6 +108,24 @@ def test_decode_repeated_calls_of_changing_batch():
         lens = uniform_lens(gen, n, 100, 2048)
         kc, vc, tables = paged_pool(gen, lens, 8 * n)
         _check(randn(gen, n, H, D), kc, vc, lens, tables, f"batch {n}")
+
+
+def test_decode_block_table_wider_than_lds():
+    """A block table of more entries than the kernel keeps in LDS (here 40 x 128 columns) is read from memory."""
+    gen = torch.Generator().manual_seed(39)
+    lens = uniform_lens(gen, 40, 1, 128 * 32)
+    kc, vc, tables = paged_pool(gen, lens, 40 * 128, block_size=32, extra_cols=128)
+    tables = tables[:, :128].contiguous()
+    tables[tables < 0] = 7
+    _check(randn(gen, 40, H, D), kc, vc, lens, tables, "wide table")
+
+
+def test_decode_batch_beyond_one_launch():
+    """More sequences than one launch's step layout holds (512): the call runs consecutive launches."""
+    gen = torch.Generator().manual_seed(38)
+    lens = uniform_lens(gen, 1100, 0, 300)
+    kc, vc, tables = paged_pool(gen, [max(n, 1) for n in lens], 1300, block_size=256)
+    _check(randn(gen, len(lens), H, D), kc, vc, lens, tables, "batch 1100")
 
 
 def test_decode_config4_layer_full_size():

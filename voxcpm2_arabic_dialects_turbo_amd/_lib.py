@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must be loaded before the library: shared HIP runti
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvoxattn.so")
 
 VOX_OK, VOX_EINVAL, VOX_EHIP = 0, 1, 2
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # every symbol include/vox_attn.h declares
 EXPORTS = (
@@ -26,8 +26,8 @@ EXPORTS = (
     "vox_store_kvcache",
     "vox_decode_attn",
     "vox_decode_workspace_bytes",
-    "vox_decode_chunk_tokens",
-    "vox_set_decode_chunk_tokens",
+    "vox_decode_workgroups",
+    "vox_set_decode_workgroups",
     "vox_prefill_attn",
 )
 
@@ -40,9 +40,9 @@ _SIGNATURES = {
                                  _i32, _i32, _c_void_p]),
     "vox_decode_attn": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _i64, _i32,
                                _c_void_p, _i32, _i32, _i32, _i32, _f32, _c_void_p, _size, _c_void_p, _c_void_p]),
-    "vox_decode_workspace_bytes": (_size, [_i32, _i32, _i32]),
-    "vox_decode_chunk_tokens": (_i32, [_i32, _i32, _i32]),
-    "vox_set_decode_chunk_tokens": (None, [_i32]),
+    "vox_decode_workspace_bytes": (_size, [_i32]),
+    "vox_decode_workgroups": (_i32, []),
+    "vox_set_decode_workgroups": (None, [_i32]),
     "vox_prefill_attn": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64,
                                 _i32, _c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32,
                                 _i32, _i32, _f32, _i32, _c_void_p, _i64, _c_void_p]),

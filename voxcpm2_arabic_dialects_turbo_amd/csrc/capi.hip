@@ -15,7 +15,7 @@
 namespace {
 
 thread_local char g_err[512] = "";
-int g_decode_chunk_override = 0;
+int g_decode_grid_override = 0;
 
 int fail(int code, const char* fmt, ...) {
   va_list ap;
@@ -63,19 +63,31 @@ int vox_store_kvcache(const void* key, const void* value, int64_t key_row_stride
                     "store_kvcache launch");
 }
 
-int vox_decode_chunk_tokens(int batch, int max_blocks, int block_size) {
-  if (g_decode_chunk_override > 0) return g_decode_chunk_override;
-  return vox::decode_chunk_tokens(batch, max_blocks * block_size);
+int vox_decode_workgroups(void) {
+  if (g_decode_grid_override > 0) return g_decode_grid_override;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+    (void)hipGetLastError();
+    cus = 256;  // MI355X
+  }
+  return cus;  // the split kernel's resident capacity: one 8-wave workgroup per CU
 }
 
-void vox_set_decode_chunk_tokens(int tokens) { g_decode_chunk_override = tokens > 0 ? tokens : 0; }
+void vox_set_decode_workgroups(int workgroups) { g_decode_grid_override = workgroups > 0 ? workgroups : 0; }
 
-size_t vox_decode_workspace_bytes(int batch, int max_blocks, int block_size) {
-  if (batch <= 0 || max_blocks <= 0 || block_size <= 0) return 0;
-  const int chunk = vox_decode_chunk_tokens(batch, max_blocks, block_size);
-  const int64_t max_ctx = (int64_t)max_blocks * block_size;
-  const int64_t max_chunks = (max_ctx + chunk - 1) / chunk;
-  return (size_t)batch * (size_t)max_chunks * vox::kPartialFloats * sizeof(float);
+namespace {
+// Workspace of one decode launch of `slice` sequences: fp32 partials [slice + grid] then the int32 step layout
+// [slice + 1], each 256-byte aligned.
+size_t decode_partials_bytes(int slice, int grid) {
+  return ((size_t)(slice + grid) * vox::kPartialFloats * sizeof(float) + 255) / 256 * 256;
+}
+}  // namespace
+
+size_t vox_decode_workspace_bytes(int batch) {
+  if (batch <= 0) return 0;
+  const int slice = batch < vox::kMaxSeqPerLaunch ? batch : vox::kMaxSeqPerLaunch;
+  return decode_partials_bytes(slice, vox_decode_workgroups()) + ((size_t)(slice + 1) * 4 + 255) / 256 * 256;
 }
 
 int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
@@ -101,12 +113,12 @@ int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, co
   if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out) || !aligned16(workspace))
     return fail(VOX_EINVAL, "decode_attn: q, caches, out and workspace must be 16-byte aligned");
   if (!std::isfinite(softmax_scale)) return fail(VOX_EINVAL, "decode_attn: softmax_scale is not finite");
-  const size_t need = vox_decode_workspace_bytes(batch, max_blocks, block_size);
-  if (workspace_bytes < need || (need && !workspace))
+  if ((int64_t)max_blocks * block_size > (1 << 30)) return fail(VOX_EINVAL, "decode_attn: block table too wide");
+  const int grid = vox_decode_workgroups();
+  const size_t need = vox_decode_workspace_bytes(batch);
+  if (workspace_bytes < need || !workspace)
     return fail(VOX_EINVAL, "decode_attn: workspace of %zu bytes, %zu needed", workspace_bytes, need);
-  const int chunk = vox_decode_chunk_tokens(batch, max_blocks, block_size);
-  if (chunk <= 0 || chunk % 64) return fail(VOX_EINVAL, "decode_attn: chunk %d not a multiple of 64", chunk);
-  const int max_ctx = max_blocks * block_size;
+  const int slice_max = batch < vox::kMaxSeqPerLaunch ? batch : vox::kMaxSeqPerLaunch;
 
   vox::DecodeArgs a;
   a.q = (const uint16_t*)q;
@@ -123,11 +135,22 @@ int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, co
   a.num_heads = num_heads;
   a.group = num_heads / num_kv_heads;
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
-  a.chunk = chunk;
-  a.max_chunks = (max_ctx + chunk - 1) / chunk;
+  a.grid = grid;
   a.partials = (float*)workspace;
+  a.steps = (int32_t*)((char*)workspace + decode_partials_bytes(slice_max, grid));
   a.out = (uint16_t*)out;
-  return hip_status(vox::launch_decode(a, num_kv_heads, max_ctx, (hipStream_t)stream), "decode_attn launch");
+  // batches beyond one launch's LDS step layout run as consecutive launches on the stream (shared workspace)
+  for (int b0 = 0; b0 < batch; b0 += vox::kMaxSeqPerLaunch) {
+    vox::DecodeArgs s = a;
+    s.batch = batch - b0 < vox::kMaxSeqPerLaunch ? batch - b0 : vox::kMaxSeqPerLaunch;
+    s.q = a.q + (int64_t)b0 * q_row_stride;
+    s.block_tables = a.block_tables + (int64_t)b0 * bt_stride;
+    s.context_lens = a.context_lens + b0;
+    s.out = a.out + (int64_t)b0 * num_heads * head_dim;
+    const int st = hip_status(vox::launch_decode(s, num_kv_heads, (hipStream_t)stream), "decode_attn launch");
+    if (st != VOX_OK) return st;
+  }
+  return VOX_OK;
 }
 
 int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const void* value,

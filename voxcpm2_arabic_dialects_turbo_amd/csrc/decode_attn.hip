@@ -6,20 +6,26 @@
 // where token j lives in cache block block_tables[b, j // block_size] at slot j % block_size, G = H / HK.
 //
 // gfx950 mapping.
-//  * A workgroup (4 waves) owns one chunk of `chunk` consecutive tokens of one sequence and ALL query heads (<= 16).
-//    A cache slot row [HK][D] is contiguous (HK * 256 bytes), so the score GEMM contracts over the whole row
-//    c = (kv head, d) with a block-diagonal query operand B[c, h] = q[h, d] if c's kv head is h's group else 0:
-//    the 16 MFMA columns are 16 real heads instead of 8 heads padded to 16, and each K slot row feeds the MFMA A
-//    operand straight from global memory (lane = token, 16 contiguous bytes per k-step).
-//  * Each wave walks 16-token tiles (K loaded into registers in MFMA layout, V coalesced; three waves per SIMD
-//    keep loads in flight): S^T[16 tok x 16 heads] = K Q^T (HK*4 MFMA 16x16x32), online softmax in fp32 with exp2, then
-//    O^T[c, h] += V^T P^T (MFMA 16x16x16 per 16 output dims and kv head). V is written row-major into a private LDS
-//    tile with 16-byte stores and read back transposed by ds_read_b64_tr_b16, which hands each lane four tokens of
-//    one column: exactly the A operand. P^T is already in the B layout, no shuffles.
-//  * Split-KV: chunks of a sequence run as independent workgroups. The four waves of a workgroup are merged in LDS;
-//    a sequence that fits one chunk is written directly, the others leave fp32 partials (O, m, l) that a small
-//    second kernel merges. Merging in the split kernel itself (last workgroup to arrive) was measured slower: every
-//    workgroup then holds its CU slot through a write-through wait and an atomic round trip.
+//  * Work split (persistent, balanced): the tokens of all sequences are cut into 64-token steps, laid end to end in
+//    sequence order, and a fixed grid of workgroups (one per CU by default) takes equal contiguous ranges of steps.
+//    Every workgroup streams the same number of bytes; it walks its range sequence by sequence. The step layout
+//    comes from a scan of context_lens inside the kernel, so the launch shape depends only on host-known sizes
+//    (graph capture). The block table is staged in LDS when it fits, so block lookups never wait on memory.
+//  * A workgroup (4 waves) computes all query heads (<= 16) of a sequence at once. A cache slot row [HK][D] is
+//    contiguous (HK * 256 bytes), so the score GEMM contracts over the whole row c = (kv head, d) with a
+//    block-diagonal query operand B[c, h] = q[h, d] if c's kv head is h's group else 0: the 16 MFMA columns are 16
+//    real heads instead of 8 heads padded to 16, and each K slot row feeds the MFMA A operand straight from global
+//    memory (lane = token, 16 contiguous bytes per k-step).
+//  * Each wave walks 16-token tiles, issuing all of a tile's loads before waiting on any: S^T[16 tok x 16 heads] = K Q^T
+//    (HK*4 MFMA 16x16x32), online softmax in fp32 with exp2, then O^T[c, h] += V^T P^T (MFMA 16x16x16 per 16 output
+//    dims and kv head). V is written row-major into a private LDS tile with 16-byte stores and read back transposed
+//    by ds_read_b64_tr_b16, which hands each lane four tokens of one column: exactly the A operand. P^T is already in
+//    the B layout, no shuffles.
+//  * Merging: the four waves of a workgroup merge in LDS. A sequence inside one workgroup's range is written
+//    directly; a sequence cut by range boundaries leaves one fp32 partial (O, m, l) per workgroup that touched it,
+//    at slot b + g (unique: the (sequence, workgroup) pairs form a monotone staircase), and decode_merge_kernel, next
+//    on the stream, combines them. (Merging in the split kernel itself, by the last workgroup to arrive, was measured
+//    slower: each workgroup then waits on a write-through and an atomic round trip.)
 #include "vox_common.h"
 #include "vox_kernels.h"
 
@@ -28,8 +34,10 @@ namespace vox {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kTile = 16;     // tokens per wave iteration
+constexpr int kTile = 16;              // tokens per wave iteration
 constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * kWave;
+constexpr int kStep = kWaves * kTile;  // tokens per workgroup step
 constexpr int kMaxHeads = 16;
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -74,8 +82,20 @@ __device__ __forceinline__ void load_tile(Tile<HK>& T, const DecodeArgs& p, int6
   }
 }
 
-template <int HK>
-__global__ __launch_bounds__(256, 3) void decode_kernel(DecodeArgs p) {
+// A value every lane of the wave holds, moved to a scalar register (LDS reads land in vector registers).
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+__device__ __forceinline__ int wave_incl_scan(int x, int lane) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int y = __shfl_up(x, o, kWave);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+template <int HK, bool BTL>
+__global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   using TT = Tile<HK>;
   constexpr int ROW = TT::ROW;
   constexpr int VROW = ROW + 16;  // padded LDS row: the 16 rows a transposed read touches hit distinct banks
@@ -84,11 +104,13 @@ __global__ __launch_bounds__(256, 3) void decode_kernel(DecodeArgs p) {
   constexpr int kRedFloats = kWaves * kMaxHeads * kD + 2 * kWaves * kMaxHeads;
   constexpr int kLdsBytes = (kVtElems * 2 > kRedFloats * 4) ? kVtElems * 2 : kRedFloats * 4;
   __shared__ __attribute__((aligned(16))) unsigned char lds_raw[kLdsBytes];
+  __shared__ int s_ctx[kMaxSeqPerLaunch];        // context per sequence, cut to the table's reach
+  __shared__ int s_start[kMaxSeqPerLaunch + 1];  // first step per sequence; s_start[batch] = total steps
+  __shared__ int s_wtot[kWaves];
+  __shared__ int s_bt[kBtLds];  // the block table, when it fits: no block-id round trips at segment starts
 
-  // Sequences vary fastest in dispatch order: chunk 0 of every sequence first, so the trailing chunk ids that most
-  // sequences do not have (early exits) are dispatched last instead of between live workgroups.
-  const int b = blockIdx.x;
-  const int c = blockIdx.y;
+  const int g = blockIdx.x;
+  const int G = gridDim.x;
   const int tid = threadIdx.x;
   const int w = tid >> 6;
   const int lane = tid & 63;
@@ -96,195 +118,272 @@ __global__ __launch_bounds__(256, 3) void decode_kernel(DecodeArgs p) {
   const int jq = lane >> 4;
   const int H = p.num_heads;
   const int max_ctx = p.max_blocks * p.block_size;
-  const int tok0 = c * p.chunk;  // < max_ctx: c < max_chunks
-  const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
 
-  // Independent loads issued together (one round trip): the context length, this lane's query row and the block
-  // id of this wave's first tile. Query row of head r16: d = kq*32 + jq*8 + [0, 8); the score B operand for k-step
-  // kc is piece kc % 4 when kc's kv head (kc / 4) is the lane's group, else zero: block-diagonal over (kv head, d).
-  const int ctx_raw = p.context_lens[b];
+  // ---- block table into LDS and the step layout (a block-wide prefix sum over ceil(context / 64)): one round trip
+  const int mb = p.max_blocks;
+  if constexpr (BTL)
+    for (int i = tid; i < p.batch * mb; i += kThreads) s_bt[i] = p.block_tables[(int64_t)(i / mb) * p.bt_stride + i % mb];
+  int run = 0;
+  for (int base = 0; base < p.batch; base += kThreads) {
+    const int bb = base + tid;
+    const int ctx = bb < p.batch ? max(0, min(p.context_lens[bb], max_ctx)) : 0;
+    const int n = (ctx + kStep - 1) / kStep;
+    const int incl = wave_incl_scan(n, lane);
+    if (lane == kWave - 1) s_wtot[w] = incl;
+    __syncthreads();
+    int before = 0, total = 0;
+#pragma unroll
+    for (int ww = 0; ww < kWaves; ++ww) {
+      before += ww < w ? s_wtot[ww] : 0;
+      total += s_wtot[ww];
+    }
+    if (bb < p.batch) {
+      s_ctx[bb] = ctx;
+      s_start[bb] = run + before + incl - n;
+    }
+    run += total;
+    __syncthreads();
+  }
+  if (tid == 0) s_start[p.batch] = run;
+  __syncthreads();
+  const int S = uniform(run);
+  if (g == 0)  // the layout decode_merge_kernel reads
+    for (int i = tid; i <= p.batch; i += kThreads) p.steps[i] = s_start[i];
+
+  // this workgroup's range [r, r1) and the sequence holding its first step: the last b with s_start[b] <= r
+  // (an empty sequence shares its start with the next one, so the last such b is not empty)
+  const int r1 = (int)((int64_t)(g + 1) * S / G);
+  int r = (int)((int64_t)g * S / G);
+  int b = 0;
+  if (r < r1) {
+    int lo = 0, hi = p.batch;  // s_start[lo] <= r < s_start[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (uniform(s_start[mid]) <= r) lo = mid; else hi = mid;
+    }
+    b = lo;
+  }
+
   const int h = r16;
   const int hg = h < H ? h / p.group : -1;
-  u32x4 qv[4];
-  {
-    const uint16_t* qb = p.q + (int64_t)b * p.q_row_stride + (int64_t)(h < H ? h : 0) * kD + jq * 8;
-#pragma unroll
-    for (int kq = 0; kq < 4; ++kq) qv[kq] = ld_g16(qb + kq * 32);
-  }
-  int64_t blk = bt_row[min(tok0 + w * kTile, max_ctx - 1) / p.block_size];
-
-  // A context longer than the block table can address is cut to it: keeps chunk ids inside the partial buffer.
-  const int ctx = min(ctx_raw, max_ctx);
-  uint16_t* out_b = p.out + (int64_t)b * H * kD;
-  if (ctx <= 0) {  // padded row of a captured batch: defined zeros
-    if (c == 0)
-      for (int i = tid; i < H * kD; i += 256) out_b[i] = 0;
-    return;
-  }
-  const int n_chunks = (ctx + p.chunk - 1) / p.chunk;
-  if (c >= n_chunks) return;
-  const int tok_end = min(ctx, tok0 + p.chunk);
-
-  float m = -INFINITY;
-  float lsum = 0.f;
-  f32x4 acc[8];
-#pragma unroll
-  for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
   uint16_t* vt = reinterpret_cast<uint16_t*>(lds_raw) + w * kTile * VROW;
   // this lane's transposed-read address inside a d-tile: row jq*4 + r16/4, column 4*(r16%4)
   const uint16_t* vtr = vt + (jq * 4 + (r16 >> 2)) * VROW + 4 * (r16 & 3);
-
-  auto compute = [&](const Tile<HK>& T, int t0) {
-    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kc = 0; kc < TT::KC; ++kc) s = mfma_16x16x32(T.k[kc], hg == kc / 4 ? qv[kc % 4] : zero4(), s);
-    // lane (head r16) holds tokens t0 + jq*4 + [0, 4)
-    float x[4];
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const bool ok = T.ok && (t0 + jq * 4 + rr) < tok_end;
-      x[rr] = ok ? s[rr] * p.scale_log2 : -INFINITY;
-      tmax = fmaxf(tmax, x[rr]);
-    }
-    tmax = col_max4(tmax);
-    const float m_new = fmaxf(m, tmax);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = fast_exp2(m - m_use);
-    float ps = 0.f;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      x[rr] = fast_exp2(x[rr] - m_use);
-      ps += x[rr];
-    }
-    lsum = lsum * alpha + ps;
-    m = m_new;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
-
-    // V tile -> LDS, row-major, 16-byte stores; rows of tokens past tok_end or of an unmapped block are zeroed
-    // (they meet p = 0 in P V, and unwritten cache slots may hold any bit pattern)
-#pragma unroll
-    for (int i = 0; i < TT::VP; ++i) {
-      const int pc = i * 64 + lane;
-      const bool ok = T.ok && (t0 + pc / TT::PPR) < tok_end;
-      *reinterpret_cast<u32x4*>(vt + (pc / TT::PPR) * VROW + (pc % TT::PPR) * 8) = ok ? T.v[i] : zero4();
-    }
-    wave_lds_sync();
-
-    // P^T operand: k-slots jq*4 + [0, 4) = tokens jq*4 + [0, 4)
-    const uint32_t p01 = pack_bf16x2(x[0], x[1]);
-    const uint32_t p23 = pack_bf16x2(x[2], x[3]);
-    const s16x4 pv = __builtin_bit_cast(s16x4, u32x2{p01, p23});
-    const s16x4 pz = s16x4{0, 0, 0, 0};
-#pragma unroll
-    for (int g = 0; g < HK; ++g) {
-      const s16x4 pb = (hg == g) ? pv : pz;
-      s16x4 va[8];
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) va[dt] = lds_read_tr16(vtr + g * kD + dt * 16);
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) acc[dt] = mfma_16x16x16(va[dt], pb, acc[dt]);
-    }
-    wave_lds_sync();
-  };
-
-  // This wave's tiles: tok0 + w*16 + k*64. Latency is hidden across waves (3 per SIMD), not inside one; the next
-  // tile's block id is read one tile ahead so each tile costs one memory round trip. Columns stay below max_blocks
-  // because the context is cut to the table's reach.
-  const int step = kWaves * kTile;
-  for (int t0 = tok0 + w * kTile; t0 < tok_end; t0 += step) {
-    const int tn = min(t0 + step, tok_end - 1);
-    const int64_t blk_next = bt_row[tn / p.block_size];
-    Tile<HK> T;
-    T.ok = blk >= 0 && blk < p.num_blocks;
-    load_tile<HK>(T, p, (T.ok ? blk : 0) * p.block_size + (t0 % p.block_size), r16, jq, lane);
-    __builtin_amdgcn_sched_barrier(0);  // all of the tile's loads issue before any of them is waited on
-    compute(T, t0);
-    blk = blk_next;
-  }
-
-  // ---- merge the four waves of this workgroup (fp32, in LDS) ----
-  lsum = col_sum4(lsum);
-  __syncthreads();
-  float* red = reinterpret_cast<float*>(lds_raw);
   constexpr int kMOff = kWaves * kMaxHeads * kD;
   constexpr int kLOff = kMOff + kWaves * kMaxHeads;
-#pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
-    *reinterpret_cast<f32x4*>(&red[(w * kMaxHeads + r16) * kD + dt * 16 + jq * 4]) = acc[dt];
-  if (jq == 0) {
-    red[kMOff + w * kMaxHeads + r16] = m;
-    red[kLOff + w * kMaxHeads + r16] = lsum;
-  }
-  __syncthreads();
 
-  const int hh = tid >> 4;        // head
-  const int d0 = (tid & 15) * 8;  // 8 consecutive dims
-  float M = -INFINITY;
-#pragma unroll
-  for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, red[kMOff + ww * kMaxHeads + hh]);
-  const float Mu = M == -INFINITY ? 0.f : M;
-  float L = 0.f;
-  float o[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = 0.f;
-#pragma unroll
-  for (int ww = 0; ww < kWaves; ++ww) {
-    const float e = fast_exp2(red[kMOff + ww * kMaxHeads + hh] - Mu);
-    L += e * red[kLOff + ww * kMaxHeads + hh];
-    const float* src = &red[(ww * kMaxHeads + hh) * kD + d0];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] += e * src[i];
-  }
-
-  if (n_chunks == 1) {
-    if (hh < H) {
-      const float inv = L > 0.f ? 1.f / L : 0.f;
-      const u32x4 ov = u32x4{pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv),
-                             pack_bf16x2(o[4] * inv, o[5] * inv), pack_bf16x2(o[6] * inv, o[7] * inv)};
-      *reinterpret_cast<u32x4*>(out_b + hh * kD + d0) = ov;
+  while (r < r1) {
+    const int ctx = uniform(s_ctx[b]);
+    const int sb = uniform(s_start[b]);
+    const int nb = uniform(s_start[b + 1]) - sb;
+    if (nb == 0) {  // an empty row holds no step
+      ++b;
+      continue;
     }
-    return;
-  }
+    const int seg_end = min(r1, sb + nb);
+    const int tok0 = (r - sb) * kStep;
+    const int tok_end = min(ctx, (seg_end - sb) * kStep);
+    const bool whole = r == sb && seg_end == sb + nb;
+    const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
+    const int* bt_lds_row = s_bt + b * mb;
+    auto block_of = [&](int col) -> int64_t {
+      if constexpr (BTL) return uniform(bt_lds_row[col]);
+      else return bt_row[col];
+    };
 
-  // ---- split-KV: publish this chunk's partial; decode_merge_kernel (next on the stream) combines them ----
-  float* part = p.partials + ((int64_t)b * p.max_chunks + c) * kPartialFloats;
-  *reinterpret_cast<f32x4*>(&part[hh * kD + d0]) = f32x4{o[0], o[1], o[2], o[3]};
-  *reinterpret_cast<f32x4*>(&part[hh * kD + d0 + 4]) = f32x4{o[4], o[5], o[6], o[7]};
-  if ((tid & 15) == 0) {
-    part[kMaxHeads * kD + hh] = M;
-    part[kMaxHeads * kD + kMaxHeads + hh] = L;
+    // The query row and the block id of this wave's first tile load together. Query row of head r16:
+    // d = kq*32 + jq*8 + [0, 8); the score B operand for k-step kc is piece kc % 4 when kc's kv head (kc / 4) is
+    // the lane's group, else zero: block-diagonal over (kv head, d).
+    u32x4 qv[4];
+    {
+      const uint16_t* qb = p.q + (int64_t)b * p.q_row_stride + (int64_t)(h < H ? h : 0) * kD + jq * 8;
+#pragma unroll
+      for (int kq = 0; kq < 4; ++kq) qv[kq] = ld_g16(qb + kq * 32);
+    }
+
+    float m = -INFINITY;
+    float lsum = 0.f;
+    f32x4 acc[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Issues the loads of the tile at token t0 of cache block blk.
+    auto issue = [&](Tile<HK>& T, int64_t blk, int t0) {
+      T.ok = blk >= 0 && blk < p.num_blocks;
+      load_tile<HK>(T, p, (T.ok ? blk : 0) * p.block_size + (t0 % p.block_size), r16, jq, lane);
+    };
+    // Scores, online softmax and P V of one loaded tile.
+    auto compute = [&](const Tile<HK>& T, int t0) {
+      f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < TT::KC; ++kc) s = mfma_16x16x32(T.k[kc], hg == kc / 4 ? qv[kc % 4] : zero4(), s);
+      // lane (head r16) holds tokens t0 + jq*4 + [0, 4)
+      float x[4];
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const bool ok = T.ok && (t0 + jq * 4 + rr) < tok_end;
+        x[rr] = ok ? s[rr] * p.scale_log2 : -INFINITY;
+        tmax = fmaxf(tmax, x[rr]);
+      }
+      tmax = col_max4(tmax);
+      const float m_new = fmaxf(m, tmax);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = fast_exp2(m - m_use);
+      float ps = 0.f;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        x[rr] = fast_exp2(x[rr] - m_use);
+        ps += x[rr];
+      }
+      lsum = lsum * alpha + ps;
+      m = m_new;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+
+      // V tile -> LDS, row-major, 16-byte stores; rows of tokens past tok_end or of an unmapped block are zeroed
+      // (they meet p = 0 in P V, and unwritten cache slots may hold any bit pattern)
+#pragma unroll
+      for (int i = 0; i < TT::VP; ++i) {
+        const int pc = i * 64 + lane;
+        const bool ok = T.ok && (t0 + pc / TT::PPR) < tok_end;
+        *reinterpret_cast<u32x4*>(vt + (pc / TT::PPR) * VROW + (pc % TT::PPR) * 8) = ok ? T.v[i] : zero4();
+      }
+      wave_lds_sync();
+
+      // P^T operand: k-slots jq*4 + [0, 4) = tokens jq*4 + [0, 4)
+      const uint32_t p01 = pack_bf16x2(x[0], x[1]);
+      const uint32_t p23 = pack_bf16x2(x[2], x[3]);
+      const s16x4 pv = __builtin_bit_cast(s16x4, u32x2{p01, p23});
+      const s16x4 pz = s16x4{0, 0, 0, 0};
+#pragma unroll
+      for (int gk = 0; gk < HK; ++gk) {
+        const s16x4 pb = (hg == gk) ? pv : pz;
+#pragma unroll
+        for (int d4 = 0; d4 < 8; d4 += 4) {
+          s16x4 va[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) va[u] = lds_read_tr16(vtr + gk * kD + (d4 + u) * 16);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) acc[d4 + u] = mfma_16x16x16(va[u], pb, acc[d4 + u]);
+        }
+      }
+      wave_lds_sync();
+    };
+
+    // This wave's tiles: first, first + kStep, ...; the block id of the next tile is read with the current tile's
+    // loads, so the loop never waits on a lookup alone.
+    const int first = tok0 + w * kTile;
+    if (first < tok_end) {
+      int64_t blk = block_of(first / p.block_size);
+      for (int t0 = first; t0 < tok_end; t0 += kStep) {
+        const int64_t blk_next = block_of(min(t0 + kStep, tok_end - 1) / p.block_size);
+        Tile<HK> T;
+        issue(T, blk, t0);
+        __builtin_amdgcn_sched_barrier(0);  // all of the tile's loads issue before any of them is waited on
+        compute(T, t0);
+        blk = blk_next;
+      }
+    }
+
+    // ---- merge the waves (fp32, in LDS); thread (head hh, dims d0 .. d0 + kDpt) ----
+    constexpr int kDpt = kMaxHeads * kD / kThreads;  // output dims per thread
+    constexpr int kTpr = kD / kDpt;                    // threads per head
+    lsum = col_sum4(lsum);
+    float* red = reinterpret_cast<float*>(lds_raw);
+    const int hh = tid / kTpr;
+    const int d0 = (tid % kTpr) * kDpt;
+    __syncthreads();
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+      *reinterpret_cast<f32x4*>(&red[(w * kMaxHeads + r16) * kD + dt * 16 + jq * 4]) = acc[dt];
+    if (jq == 0) {
+      red[kMOff + w * kMaxHeads + r16] = m;
+      red[kLOff + w * kMaxHeads + r16] = lsum;
+    }
+    __syncthreads();
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, red[kMOff + ww * kMaxHeads + hh]);
+    const float Mu = M == -INFINITY ? 0.f : M;
+    float L = 0.f;
+    f32x4 o[kDpt / 4];
+#pragma unroll
+    for (int i = 0; i < kDpt / 4; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ww = 0; ww < kWaves; ++ww) {
+      const float e = fast_exp2(red[kMOff + ww * kMaxHeads + hh] - Mu);
+      L += e * red[kLOff + ww * kMaxHeads + hh];
+#pragma unroll
+      for (int i = 0; i < kDpt / 4; ++i)
+        o[i] += e * *reinterpret_cast<const f32x4*>(&red[(ww * kMaxHeads + hh) * kD + d0 + 4 * i]);
+    }
+    if (whole) {
+      if (hh < H) {
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+        for (int i = 0; i < kDpt / 4; ++i)
+          *reinterpret_cast<u32x2*>(p.out + ((int64_t)b * H + hh) * kD + d0 + 4 * i) =
+              u32x2{pack_bf16x2(o[i][0] * inv, o[i][1] * inv), pack_bf16x2(o[i][2] * inv, o[i][3] * inv)};
+      }
+    } else {  // cut by a range boundary: partial for decode_merge_kernel, slot b + g
+      float* part = p.partials + (int64_t)(b + g) * kPartialFloats;
+#pragma unroll
+      for (int i = 0; i < kDpt / 4; ++i) *reinterpret_cast<f32x4*>(&part[hh * kD + d0 + 4 * i]) = o[i];
+      if (tid % kTpr == 0) {
+        part[kMaxHeads * kD + hh] = M;
+        part[kMaxHeads * kD + kMaxHeads + hh] = L;
+      }
+    }
+    __syncthreads();  // LDS is free for the next sequence
+
+    r = seg_end;
+    ++b;
   }
 }
 
-// Combines the chunk partials of every sequence that the decode kernel split (n_chunks > 1): online rescale over
-// the chunks (fp32), normalize, bf16. One workgroup per sequence, thread = (head, 8 dims); partial loads of four
-// chunks are issued together. Runs after decode_kernel on the same stream, which makes the partials visible.
+// Writes the sequences that decode_kernel left as partials, and the zeros of empty rows. One workgroup per
+// sequence, thread = (head, 8 dims). Sequence b covers steps [sb, eb) of the layout decode_kernel published in
+// `steps`; workgroup g of G covers
+// [floor(g S / G), floor((g + 1) S / G)); the workgroups touching b are g_first..g_last below, each left a partial at
+// slot b + g unless its range is empty. Online rescale over the partials (fp32), partial loads of four workgroups
+// in flight together. Runs after decode_kernel on the same stream, which makes the partials visible.
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs p) {
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
   const int hh = tid >> 4;
   const int d0 = (tid & 15) * 8;
-  const int ctx = min(p.context_lens[b], p.max_blocks * p.block_size);
-  const int n_chunks = (ctx + p.chunk - 1) / p.chunk;
-  if (n_chunks <= 1 || hh >= p.num_heads) return;
-  const float* pb = p.partials + (int64_t)b * p.max_chunks * kPartialFloats;
+  const int H = p.num_heads;
+  const int64_t S = p.steps[p.batch];
+  const int64_t sb = p.steps[b];
+  const int64_t eb = p.steps[b + 1];
+  uint16_t* ob = p.out + ((int64_t)b * H + hh) * kD + d0;
+  if (hh >= H) return;
+  if (eb == sb) {  // empty (padded) row: defined zeros
+    *reinterpret_cast<u32x4*>(ob) = zero4();
+    return;
+  }
+  const int64_t G = p.grid;
+  const int g_first = (int)(((sb + 1) * G + S - 1) / S) - 1;
+  const int g_last = (int)min(G - 1, (eb * G + S - 1) / S - 1);
+  if (g_first >= g_last) return;  // one workgroup held the whole sequence and wrote it
+
   float M2 = -INFINITY, L2 = 0.f;
   float o2[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) o2[i] = 0.f;
-  for (int c0 = 0; c0 < n_chunks; c0 += 4) {
+  for (int g0 = g_first; g0 <= g_last; g0 += 4) {
     float mc[4], lc[4];
-    f32x4 oa[4], ob[4];
+    f32x4 oa[4], obv[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const float* pc = pb + (int64_t)min(c0 + u, n_chunks - 1) * kPartialFloats;
-      mc[u] = (c0 + u < n_chunks) ? pc[kMaxHeads * kD + hh] : -INFINITY;
-      lc[u] = pc[kMaxHeads * kD + kMaxHeads + hh];
-      oa[u] = *reinterpret_cast<const f32x4*>(&pc[hh * kD + d0]);
-      ob[u] = *reinterpret_cast<const f32x4*>(&pc[hh * kD + d0 + 4]);
+      const int64_t gg = min(g0 + u, g_last);
+      const bool live = g0 + u <= g_last && (gg * S / G) < ((gg + 1) * S / G);  // an empty range wrote nothing
+      const float* pc = p.partials + (b + gg) * kPartialFloats;
+      mc[u] = live ? pc[kMaxHeads * kD + hh] : -INFINITY;
+      lc[u] = live ? pc[kMaxHeads * kD + kMaxHeads + hh] : 0.f;
+      oa[u] = live ? *reinterpret_cast<const f32x4*>(&pc[hh * kD + d0]) : f32x4{0.f, 0.f, 0.f, 0.f};
+      obv[u] = live ? *reinterpret_cast<const f32x4*>(&pc[hh * kD + d0 + 4]) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -296,40 +395,32 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         o2[i] = o2[i] * a + e * oa[u][i];
-        o2[i + 4] = o2[i + 4] * a + e * ob[u][i];
+        o2[i + 4] = o2[i + 4] * a + e * obv[u][i];
       }
       M2 = mn;
     }
   }
   const float inv = L2 > 0.f ? 1.f / L2 : 0.f;
-  const u32x4 ov = u32x4{pack_bf16x2(o2[0] * inv, o2[1] * inv), pack_bf16x2(o2[2] * inv, o2[3] * inv),
-                         pack_bf16x2(o2[4] * inv, o2[5] * inv), pack_bf16x2(o2[6] * inv, o2[7] * inv)};
-  *reinterpret_cast<u32x4*>(p.out + ((int64_t)b * p.num_heads + hh) * kD + d0) = ov;
+  *reinterpret_cast<u32x4*>(ob) =
+      u32x4{pack_bf16x2(o2[0] * inv, o2[1] * inv), pack_bf16x2(o2[2] * inv, o2[3] * inv),
+            pack_bf16x2(o2[4] * inv, o2[5] * inv), pack_bf16x2(o2[6] * inv, o2[7] * inv)};
 }
 
 }  // namespace
 
-int decode_chunk_tokens(int batch, int max_ctx) {
-  // Chunks are multiples of one 4-wave x 16-token step. Prefer 256-token chunks (fewer partials to merge), halve
-  // them while the grid would leave the 256 CUs with less than ~4 workgroups each.
-  int chunk = 256;
-  while (chunk > kWaves * kTile * 2) {
-    const int64_t wgs = (int64_t)batch * ((max_ctx + chunk - 1) / chunk);
-    if (wgs >= 1024) break;
-    chunk /= 2;
-  }
-  return chunk;
-}
-
-hipError_t launch_decode(const DecodeArgs& a, int num_kv_heads, int max_ctx, hipStream_t stream) {
-  const int n_chunks = (max_ctx + a.chunk - 1) / a.chunk;
-  dim3 grid((unsigned)a.batch, (unsigned)(n_chunks > 0 ? n_chunks : 1));
-  if (num_kv_heads == 1)
-    decode_kernel<1><<<grid, dim3(256), 0, stream>>>(a);
+hipError_t launch_decode(const DecodeArgs& a, int num_kv_heads, hipStream_t stream) {
+  const dim3 grid((unsigned)a.grid);
+  const bool btl = (int64_t)a.batch * a.max_blocks <= kBtLds;
+  if (num_kv_heads == 1 && btl)
+    decode_kernel<1, true><<<grid, dim3(kThreads), 0, stream>>>(a);
+  else if (num_kv_heads == 1)
+    decode_kernel<1, false><<<grid, dim3(kThreads), 0, stream>>>(a);
+  else if (btl)
+    decode_kernel<2, true><<<grid, dim3(kThreads), 0, stream>>>(a);
   else
-    decode_kernel<2><<<grid, dim3(256), 0, stream>>>(a);
+    decode_kernel<2, false><<<grid, dim3(kThreads), 0, stream>>>(a);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || n_chunks <= 1) return e;
+  if (e != hipSuccess) return e;
   decode_merge_kernel<<<dim3((unsigned)a.batch), dim3(256), 0, stream>>>(a);
   return hipGetLastError();
 }

@@ -6,8 +6,12 @@
 
 namespace vox {
 
-// One decode partial per (sequence, chunk): O[16 heads][128] unnormalized, then m[16] and l[16] (log2 domain).
+// One decode partial: O[16 heads][128] unnormalized, then m[16] and l[16] (log2 domain).
 constexpr int kPartialFloats = 16 * 128 + 16 + 16;
+// Sequences one decode launch takes (their step layout lives in LDS); larger batches are launched in slices.
+constexpr int kMaxSeqPerLaunch = 512;
+// Block-table entries (batch x max_blocks) a decode launch keeps in LDS; wider tables are read from global memory.
+constexpr int kBtLds = 3584;
 
 struct DecodeArgs {
   const uint16_t* q;          // bf16 [B, H, 128]; sequence rows q_row_stride apart, heads 128 apart
@@ -24,9 +28,9 @@ struct DecodeArgs {
   int num_heads;
   int group;                  // H / HK
   float scale_log2;           // softmax_scale * log2(e)
-  int chunk;                  // tokens per workgroup (multiple of 64)
-  int max_chunks;             // ceil(max_blocks * block_size / chunk)
-  float* partials;            // [B, max_chunks, kPartialFloats]
+  int grid;                   // workgroups of the split kernel (persistent, balanced ranges)
+  float* partials;            // [B + grid, kPartialFloats]
+  int32_t* steps;             // [B + 1]: first 64-token step of every sequence, then the total
   uint16_t* out;              // bf16 [B, H, 128], contiguous
 };
 
@@ -65,8 +69,7 @@ hipError_t launch_store_kvcache(const void* k, const void* v, int64_t k_row_stri
                                 void* k_cache, void* v_cache, int64_t num_slots, const int32_t* slot_mapping,
                                 int64_t n, int row_elems, bool vec16, hipStream_t stream);
 
-int decode_chunk_tokens(int batch, int max_ctx);
-hipError_t launch_decode(const DecodeArgs& a, int num_kv_heads, int max_ctx, hipStream_t stream);
+hipError_t launch_decode(const DecodeArgs& a, int num_kv_heads, hipStream_t stream);
 
 hipError_t launch_prefill(const PrefillArgs& a, int max_seqlen_q, hipStream_t stream);
 

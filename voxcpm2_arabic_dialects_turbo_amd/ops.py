@@ -109,7 +109,7 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     lens = _as_i32(context_lens.reshape(-1), "context_lens")
     max_blocks = bt.shape[1]
     lib = _lib.load()
-    ws_bytes = lib.vox_decode_workspace_bytes(B, max_blocks, block_size)
+    ws_bytes = lib.vox_decode_workspace_bytes(B)
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
     _lib.check(lib.vox_decode_attn(q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), num_blocks,
                                    block_size, bt.data_ptr(), bt.stride(0), max_blocks, lens.data_ptr(), B, H, HK, D,
