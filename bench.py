@@ -22,6 +22,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -265,6 +266,21 @@ def cpu_baseline(w, budget_s: float):
                 ms_per_step_extrapolated=round(spent / done * 28 * 1e3, 1))
 
 
+TRAFFIC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "decode_config4_hbm_traffic.md")
+
+
+def _profiled_traffic():
+    """HBM bytes of one decode call, as measured by the rocprofv3 FETCH_SIZE / WRITE_SIZE runs summarized in
+    profiles/ (copy-calibrated; the line `traffic_bytes_per_call: N`); None when no summary is present."""
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            m = re.search(r"traffic_bytes_per_call:\s*(\d+)", f.read())
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -315,12 +331,12 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_kernel<2> + decode_merge_kernel (one decode call)",
+            "kernel": "decode_kernel<2, true> + decode_merge_kernel (one decode call)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": _profiled_traffic(),
             "launch_us": round(res["launch_ms"] * 1e3, 2),
             "launch_bytes": res["launch_bytes"],
         },

@@ -59,8 +59,9 @@ int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, co
  * counterpart: flash-attn sizes its split-KV buffers internally (reference call site: nanovllm_voxcpm/model/layers.py:350). */
 size_t vox_decode_workspace_bytes(int batch);
 
-/* Workgroups the decode split kernel runs on the current device (3 per CU), and a process-wide override for tuning
- * and tests (0 restores the built-in choice). No reference counterpart. */
+/* Workgroups the decode split kernel runs on the current device (one per CU), and a process-wide override for tuning
+ * and tests (0 restores the built-in choice; change it only between calls, the workspace size depends on it). No
+ * reference counterpart. */
 int vox_decode_workgroups(void);
 void vox_set_decode_workgroups(int workgroups);
 
