@@ -217,6 +217,21 @@ def bench_prefill(dev):
                           pct_mfma_peak=round(100 * tf / MFMA_BF16_PEAK_TFLOPS, 2),
                           flop_per_byte=round(flops / nbytes, 1), roofline_bound_tflops=round(bound, 1),
                           pct_of_roofline_bound=round(100 * tf / bound, 2), input_sets=n_sets)
+    # the same launches with the int8 output epilogue (o * inv_smooth -> int8 + per-token scale, the W8A8 o_proj's
+    # input); the output bytes shrink to T x (H x D + 4)
+    inv_smooth = torch.rand(H * D, generator=torch.Generator(device=dev).manual_seed(52), device=dev) + 0.5
+
+    def run_c2_int8():
+        for s in range(n_sets):
+            q, k, v = qkv[s].split([H * D, HK * D, HK * D], dim=-1)
+            varlen_attention(q.view(T, H, D), k.view(T, HK, D), v.view(T, HK, D), cu_seqlens_q=cu, cu_seqlens_k=cu,
+                             max_seqlen_q=max(lens), softmax_scale=SCALE, causal=True, quant=True,
+                             inv_smooth=inv_smooth)
+
+    ms8 = _graph_ms(run_c2_int8, 20) / n_sets
+    tf8 = flops / (ms8 * 1e-3) / 1e12
+    out["config2_int8_output"] = dict(launch_us=round(ms8 * 1e3, 2), tflops=round(tf8, 2),
+                                      pct_mfma_peak=round(100 * tf8 / MFMA_BF16_PEAK_TFLOPS, 2))
     del qkv
     # supplementary compute-bound shape: 16 sequences x 2048 tokens, causal
     L, NB = 2048, 16

@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define VOX_ABI_VERSION 3
+#define VOX_ABI_VERSION 4
 
 #define VOX_OK 0
 #define VOX_EINVAL 1 /* bad argument: shape, stride, alignment or null pointer (reference: the asserts of
@@ -84,6 +84,23 @@ int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const
                      int max_seqlen_q, int uniform_seqlen_q, int uniform_seqlen_k, int num_heads, int num_kv_heads,
                      int head_dim, float softmax_scale, int causal, void* out, int64_t out_row_stride,
                      void* stream);
+
+/* vox_prefill_attn with the int8 output epilogue the W8A8 o_proj consumes. Replaces the quant=True modes of the
+ * Triton paged_prefill_attention, short_causal_attention and short_attention (reference:
+ * nanovllm_voxcpm/kernels/prefill_attn.py:84-92 and :98-124, kernels/short_attn.py:55-64, :70-90, :137-146, :156-179;
+ * caller kernels/fused_layer.py:698-730). Per token t, with o the fp32 attention output over all heads:
+ *   x = o * inv_smooth (inv_smooth fp32 [num_heads * head_dim], NULL = 1), amax = max(max_c |x[c]|, 1e-6),
+ *   out_scale[t] = amax / 127,   out_q[t, c] = rint(x[c] / out_scale[t])  (round half to even, int8).
+ *   out_q      int8 [T, num_heads * head_dim], token rows out_q_row_stride apart (multiple of 4, 4-byte aligned)
+ *   out_scale  fp32 [T]
+ * Other arguments as vox_prefill_attn. Supported: num_kv_heads 1 or 2 (one workgroup holds all heads of its tokens). */
+int vox_prefill_attn_int8(const void* q, int64_t q_row_stride, const void* key, const void* value,
+                          int64_t key_row_stride, int64_t value_row_stride, const void* k_cache, const void* v_cache,
+                          int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
+                          int max_blocks, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch,
+                          int max_seqlen_q, int uniform_seqlen_q, int uniform_seqlen_k, int num_heads,
+                          int num_kv_heads, int head_dim, float softmax_scale, int causal, const float* inv_smooth,
+                          void* out_q, int64_t out_q_row_stride, float* out_scale, void* stream);
 
 #ifdef __cplusplus
 }

@@ -108,6 +108,23 @@ def dense(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float | None
     return torch.stack([attend(q[b], k[b], v[b], causal=causal, scale=scale).view(L, H, D) for b in range(B)])
 
 
+def quantize_rows(x: torch.Tensor, inv_smooth: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row int8 quantization the W8A8 o_proj consumes: x [M, K] (fp32) -> (int8 [M, K], fp32 scale [M]) with
+    y = x * inv_smooth, amax = max(max |y|, 1e-6), scale = amax / 127, q = rint(y / scale) (round half to even).
+    Reference: nanovllm_voxcpm/kernels/int8_linear.py:19-30 (``_quant_rows``), the same epilogue as
+    kernels/prefill_attn.py:84-92 and kernels/short_attn.py:55-64, 137-146 apply to the attention output."""
+    y = x.float() if inv_smooth is None else x.float() * inv_smooth.float().reshape(1, -1)
+    amax = y.abs().amax(dim=1).clamp_min(1e-6)
+    scale = amax / 127.0
+    q = torch.round(y / scale[:, None])  # torch.round rounds half to even, as rint
+    return q.to(torch.int8), scale
+
+
+def dequantize_rows(q: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """q * scale per row (reference: tests/test_kernel_references.py:162-163, ``_deq``)."""
+    return q.float() * scale.float()[:, None]
+
+
 def close(out: torch.Tensor, ref: torch.Tensor, rel: float) -> float:
     """max|out - ref| <= rel * max|ref| (reference: tests/test_kernel_references.py:51-55); returns the ratio."""
     err = (out.float() - ref.float()).abs().max().item()

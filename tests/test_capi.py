@@ -115,6 +115,32 @@ def test_prefill_rejects_bad_arguments():
     assert lib.vox_prefill_attn(*zero) == _lib.VOX_OK
 
 
+def test_prefill_int8_rejects_bad_arguments():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    # valid apart from the fake pointers: never passed unmodified (it would launch)
+    args = [p, 2048, p, p, 256, 256, None, None, 0, 0, None, 0, 0, p, p, 2, 16, 0, 0, 16, 2, 128, 0.088, 1, None, p,
+            2048, p, None]
+    bad = list(args)
+    bad[20], bad[19] = 4, 16  # four KV heads: one workgroup would need 1024 threads
+    assert lib.vox_prefill_attn_int8(*bad) == _lib.VOX_EINVAL and "num_kv_heads" in _err()
+    bad = list(args)
+    bad[27] = None  # no scale output
+    assert lib.vox_prefill_attn_int8(*bad) == _lib.VOX_EINVAL and "out_scale" in _err()
+    bad = list(args)
+    bad[26] = 2046  # row stride not a multiple of 4
+    assert lib.vox_prefill_attn_int8(*bad) == _lib.VOX_EINVAL and "out_q" in _err()
+    bad = list(args)
+    bad[24] = ctypes.c_void_p(260)  # inv_smooth not 16-byte aligned
+    assert lib.vox_prefill_attn_int8(*bad) == _lib.VOX_EINVAL and "inv_smooth" in _err()
+    bad = list(args)
+    bad[21] = 64  # head_dim, from the shared prefill checks
+    assert lib.vox_prefill_attn_int8(*bad) == _lib.VOX_EINVAL and "head_dim" in _err()
+    zero = list(args)
+    zero[15] = 0
+    assert lib.vox_prefill_attn_int8(*zero) == _lib.VOX_OK
+
+
 def test_python_errors_carry_the_library_message():
     with pytest.raises(ValueError, match="head_dim"):
         _lib.check(_decode(d=64), "decode_attn")

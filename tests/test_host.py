@@ -228,10 +228,11 @@ def test_reference_kernel_mirrors_keep_their_contracts():
     cu = torch.tensor([0, 3], dtype=torch.int32)
     with pytest.raises(AssertionError):
         short_causal_attention(q, kv, kv, cu, 33, 0.1)  # SHORT_CAUSAL_MAX_LEN
-    with pytest.raises(NotImplementedError):
+    # the int8 modes exist; on CPU tensors they stop at the device check, before any kernel (no CPU fallback)
+    with pytest.raises(ValueError, match="GPU"):
         short_causal_attention(q, kv, kv, cu, 3, 0.1, quant=True)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError, match="GPU"):
         short_attention(q.view(1, 3, 16, 128), kv.view(1, 3, 2, 128), kv.view(1, 3, 2, 128), 0.1, quant=True)
     cache = torch.zeros(2, 256, 2, 128, dtype=torch.bfloat16)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError, match="GPU"):
         paged_prefill_attention(q, cache, cache, torch.zeros(1, 1, dtype=torch.int32), cu, cu, 3, 0.1, quant=True)

@@ -259,3 +259,42 @@ def test_decode_context_hand_computed():
     assert slots == [2 * 4 + 1, 5 * 4 + 3, 9 * 4 + 0]
     assert lens == [6, 4, 9]
     assert tables == [[7, 2, -1], [5, -1, -1], [1, 3, 9]]
+
+
+# --- int8 output epilogue (quantize_rows) -------------------------------------------------------------------------
+
+def test_quantize_rows_closed_form_and_half_to_even():
+    """amax 127 gives scale 1 exactly, so q = rint(y): halves go to the even neighbour (a round-half-away oracle
+    would give -3, 3 for -2.5, 2.5)."""
+    x = torch.tensor([[127.0, -2.5, 2.5, 3.5, -3.5, 0.49, 1.5, -126.5]])
+    q, scale = ref.quantize_rows(x)
+    assert scale.tolist() == [1.0]
+    assert q.tolist() == [[127, -2, 2, 4, -4, 0, 2, -126]]
+    assert q.dtype == torch.int8 and scale.dtype == torch.float32
+
+
+def test_quantize_rows_zero_row_and_smoothing():
+    q, scale = ref.quantize_rows(torch.zeros(1, 6))
+    assert q.abs().sum() == 0 and scale.item() == pytest.approx(1e-6 / 127, rel=1e-6)
+    inv = torch.tensor([1.0, 2.0, 0.5, 4.0])
+    q, scale = ref.quantize_rows(torch.ones(2, 4), inv)  # y = inv_smooth itself: amax 4
+    assert scale.tolist() == [float(np.float32(4.0) / np.float32(127.0))] * 2
+    assert q[0].tolist() == [round(127 / 4), round(127 / 2), round(127 / 8), 127]
+
+
+def test_quantize_rows_matches_an_elementwise_loop():
+    """Per-element restatement in numpy float32 with Python's round (half to even) on random rows."""
+    gen = torch.Generator().manual_seed(7)
+    x = torch.randn(5, 48, generator=gen) * torch.tensor([0.01, 1.0, 30.0, 1e-7, 5.0])[:, None]
+    inv = torch.rand(48, generator=gen) + 0.5
+    q, scale = ref.quantize_rows(x, inv)
+    xs, invs = x.numpy().astype(np.float32), inv.numpy().astype(np.float32)
+    for i in range(5):
+        y = [np.float32(xs[i, j]) * invs[j] for j in range(48)]
+        amax = max(max(abs(v) for v in y), np.float32(1e-6))
+        s = np.float32(amax) / np.float32(127.0)
+        assert np.float32(scale[i].item()) == s
+        assert q[i].tolist() == [int(round(float(np.float32(v) / s))) for v in y]
+        # the reference test's bound on the dequantized row (tests/test_kernel_references.py:206-209)
+        err = (ref.dequantize_rows(q[i:i + 1], scale[i:i + 1]) - x[i:i + 1] * inv).abs()
+        assert bool((err <= 0.51 * scale[i]).all())

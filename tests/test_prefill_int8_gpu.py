@@ -1,0 +1,105 @@
+"""GPU parity of the prefill kernel's int8 output epilogue (the quant=True modes of the reference's Triton
+paged_prefill_attention, short_causal_attention and short_attention) against the oracle: fp32 attention, then the
+reference's per-token quantization (oracle.attention.quantize_rows).
+
+Bounds per token row (scale = the oracle's per-token scale):
+- scale: relative error <= 1e-2 (the amax of an output whose elements are within the attention tolerance);
+- dequantized int8 vs the fp32 oracle output: <= 0.51 * scale + 0.02 * max|ref| everywhere (the reference test's own
+  bound, tests/test_kernel_references.py:206-209), and mean error <= 0.3 * mean(scale) + 2e-3;
+- int8 codes: at most 1% of them differ from the oracle's codes by more than one step.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import attention as ref
+from tests._util import D, H, HK, paged_pool, randn, uniform_lens
+from tests.golden import make_golden
+from voxcpm2_arabic_dialects_turbo_amd.kernels.prefill_attn import paged_prefill_attention
+from voxcpm2_arabic_dialects_turbo_amd.kernels.short_attn import short_attention, short_causal_attention
+from voxcpm2_arabic_dialects_turbo_amd.ops import varlen_attention
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+SCALE = D ** -0.5
+
+
+def _check(out, want, what, inv_smooth=None):
+    """out = (int8 [T, H*D], fp32 [T]) from the GPU; want = fp32 attention output [T, H*D] (or [T, H, D])."""
+    q, scale = out
+    T = scale.numel()
+    assert q.dtype == torch.int8 and scale.dtype == torch.float32 and q.shape == (T, want.numel() // T)
+    want = want.reshape(T, -1).float()
+    q_ref, s_ref = ref.quantize_rows(want, inv_smooth)
+    y = want if inv_smooth is None else want * inv_smooth.float().cpu()
+    q, scale = q.cpu(), scale.cpu()
+    rel = ((scale - s_ref).abs() / s_ref).max().item()
+    assert rel <= 1e-2, f"{what}: scale relative error {rel:.3g}"
+    err = (ref.dequantize_rows(q, scale) - y).abs()
+    bound = 0.51 * s_ref[:, None] + 0.02 * y.abs().max()
+    assert bool((err <= bound).all()), f"{what}: dequantized error {err.max().item():.3g}"
+    assert err.mean().item() <= 0.3 * s_ref.mean().item() + 2e-3, f"{what}: mean error {err.mean().item():.3g}"
+    off = ((q.int() - q_ref.int()).abs() > 1).float().mean().item()
+    assert off <= 0.01, f"{what}: {off:.2%} of codes more than one step from the oracle's"
+
+
+@pytest.mark.parametrize("smooth", [False, True])
+def test_paged_prefill_int8_reference_case(smooth):
+    """tests/test_kernel_references.py:179-207 with quant=True (and an inv_smooth vector)."""
+    inp = make_golden.inputs("paged_prefill")
+    d = {k: (v.to(DEV) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    inv = (torch.rand(H * D, generator=torch.Generator().manual_seed(70)) + 0.5) if smooth else None
+    out = paged_prefill_attention(d["q"], d["k_cache"], d["v_cache"], d["tables"], d["cu_q"], d["cu_k"], 7, SCALE,
+                                  quant=True, inv_smooth=None if inv is None else inv.to(DEV))
+    want = ref.varlen(inp["q"].float(), inp["cu_q"], inp["cu_k"], k_cache=inp["k_cache"], v_cache=inp["v_cache"],
+                      block_tables=inp["tables"])
+    _check(out, want, "paged prefill int8", inv)
+
+
+def test_short_causal_int8_reference_case():
+    """tests/test_kernel_references.py:210-228 with quant=True: packed lens [1, 7, 16, 32, 3]."""
+    inp = make_golden.inputs("short_causal")
+    out = short_causal_attention(inp["q"].to(DEV), inp["k"].to(DEV), inp["v"].to(DEV), inp["cu"].to(DEV), 32, SCALE,
+                                 quant=True)
+    _check(out, ref.varlen(inp["q"].float(), inp["cu"], inp["cu"], k=inp["k"], v=inp["v"]), "short causal int8")
+
+
+@pytest.mark.parametrize("L", [1, 5, 11, 16])
+def test_short_non_causal_int8(L):
+    """tests/test_kernel_references.py:230-236 with quant=True: 6 rows of L tokens, non-causal."""
+    gen = torch.Generator().manual_seed(71 + L)
+    q, k, v = randn(gen, 6, L, H, D), randn(gen, 6, L, HK, D), randn(gen, 6, L, HK, D)
+    out = short_attention(q.to(DEV), k.to(DEV), v.to(DEV), SCALE, quant=True)
+    _check(out, ref.dense(q.float(), k.float(), v.float()).reshape(6 * L, -1), f"short L={L} int8")
+
+
+def test_config2_packed_int8_with_smoothing():
+    """BASELINE config 2 shape (8 packed causal sequences, L ~ U[64, 512]), int8 output with inv_smooth."""
+    gen = torch.Generator().manual_seed(72)
+    lens = uniform_lens(gen, 8, 64, 512)
+    T = sum(lens)
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32)
+    q, k, v = randn(gen, T, H, D), randn(gen, T, HK, D), randn(gen, T, HK, D)
+    inv = torch.rand(H * D, generator=gen) * 2 + 0.25
+    out = varlen_attention(q.to(DEV), k.to(DEV), v.to(DEV), cu_seqlens_q=cu.to(DEV), cu_seqlens_k=cu.to(DEV),
+                           max_seqlen_q=max(lens), softmax_scale=SCALE, causal=True, quant=True,
+                           inv_smooth=inv.to(DEV))
+    _check(out, ref.varlen(q.float(), cu, cu, k=k, v=v), "config 2 int8", inv)
+
+
+def test_paged_int8_one_kv_head_and_zero_length_rows():
+    """8 query heads over 1 KV head (tensor parallel 2), paged with a cached prefix, and padded zero-length
+    sequences, whose rows are not written."""
+    gen = torch.Generator().manual_seed(73)
+    nq, nk = [9, 0, 40, 0, 1], [300, 0, 40, 0, 77]
+    kc, vc, tables = paged_pool(gen, [max(n, 1) for n in nk], 12, hk=1)
+    T = sum(nq)
+    q = randn(gen, T, 8, D)
+    cu_q = torch.tensor([0] + torch.tensor(nq).cumsum(0).tolist(), dtype=torch.int32)
+    cu_k = torch.tensor([0] + torch.tensor(nk).cumsum(0).tolist(), dtype=torch.int32)
+    out = paged_prefill_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), tables.to(DEV), cu_q.to(DEV), cu_k.to(DEV),
+                                  max(nq), SCALE, quant=True)
+    want = ref.varlen(q.float(), cu_q, cu_k, k_cache=kc, v_cache=vc, block_tables=tables)
+    _check(out, want, "HK=1 paged int8")

@@ -153,6 +153,72 @@ int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, co
   return VOX_OK;
 }
 
+}  // extern "C"
+
+namespace {
+// Validates a prefill call's shared arguments (all but the output) and fills its launch descriptor.
+int prefill_setup(const char* fn, const void* q, int64_t q_row_stride, const void* key, const void* value,
+                  int64_t key_row_stride, int64_t value_row_stride, const void* k_cache, const void* v_cache,
+                  int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride, int max_blocks,
+                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch, int max_seqlen_q,
+                  int uniform_seqlen_q, int uniform_seqlen_k, int num_heads, int num_kv_heads, int head_dim,
+                  float softmax_scale, int causal, vox::PrefillArgs* a) {
+  if (!q) return fail(VOX_EINVAL, "%s: null q", fn);
+  if (head_dim != kHeadDim) return fail(VOX_EINVAL, "%s: head_dim %d unsupported (128 only)", fn, head_dim);
+  if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads)
+    return fail(VOX_EINVAL, "%s: num_heads %d not a multiple of num_kv_heads %d", fn, num_heads, num_kv_heads);
+  const int group = num_heads / num_kv_heads;
+  if (128 % group) return fail(VOX_EINVAL, "%s: group size %d must divide 128", fn, group);
+  if ((cu_seqlens_q == nullptr) != (cu_seqlens_k == nullptr))
+    return fail(VOX_EINVAL, "%s: give both cu_seqlens or neither", fn);
+  if (!cu_seqlens_q && (uniform_seqlen_q <= 0 || uniform_seqlen_k <= 0))
+    return fail(VOX_EINVAL, "%s: uniform lengths must be positive without cu_seqlens", fn);
+  if (!cu_seqlens_q && max_seqlen_q != uniform_seqlen_q)
+    return fail(VOX_EINVAL, "%s: max_seqlen_q must equal the uniform length", fn);
+  if (q_row_stride < (int64_t)num_heads * head_dim || q_row_stride % 8 || !aligned16(q))
+    return fail(VOX_EINVAL, "%s: q must be 16-byte aligned with a row stride >= H*D, multiple of 8", fn);
+  if (!std::isfinite(softmax_scale)) return fail(VOX_EINVAL, "%s: softmax_scale is not finite", fn);
+  if (block_tables) {
+    if (!k_cache || !v_cache) return fail(VOX_EINVAL, "%s: block tables without caches", fn);
+    if (block_size <= 0 || max_blocks <= 0 || bt_stride < max_blocks || num_blocks <= 0)
+      return fail(VOX_EINVAL, "%s: bad block table or cache shape", fn);
+    if (!aligned16(k_cache) || !aligned16(v_cache)) return fail(VOX_EINVAL, "%s: caches not aligned", fn);
+  } else {
+    if (!key || !value) return fail(VOX_EINVAL, "%s: null key/value without block tables", fn);
+    if (key_row_stride < (int64_t)num_kv_heads * head_dim || value_row_stride < (int64_t)num_kv_heads * head_dim ||
+        key_row_stride % 8 || value_row_stride % 8 || !aligned16(key) || !aligned16(value))
+      return fail(VOX_EINVAL, "%s: key/value must be 16-byte aligned rows, stride multiple of 8", fn);
+  }
+  *a = vox::PrefillArgs{};
+  a->q = (const uint16_t*)q;
+  a->q_row_stride = q_row_stride;
+  a->k_src = (const uint16_t*)key;
+  a->v_src = (const uint16_t*)value;
+  a->k_row_stride = key_row_stride;
+  a->v_row_stride = value_row_stride;
+  a->k_cache = (const uint16_t*)k_cache;
+  a->v_cache = (const uint16_t*)v_cache;
+  a->num_blocks = num_blocks;
+  a->block_size = block_size;
+  a->block_tables = block_tables;
+  a->bt_stride = bt_stride;
+  a->max_blocks = max_blocks;
+  a->cu_q = cu_seqlens_q;
+  a->cu_k = cu_seqlens_k;
+  a->uniform_q = uniform_seqlen_q;
+  a->uniform_k = uniform_seqlen_k;
+  a->batch = batch;
+  a->num_heads = num_heads;
+  a->num_kv_heads = num_kv_heads;
+  a->group = group;
+  a->scale_log2 = softmax_scale * 1.4426950408889634f;
+  a->causal = causal ? 1 : 0;
+  return VOX_OK;
+}
+}  // namespace
+
+extern "C" {
+
 int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const void* value,
                      int64_t key_row_stride, int64_t value_row_stride, const void* k_cache, const void* v_cache,
                      int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
@@ -162,63 +228,47 @@ int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const
                      void* stream) {
   if (batch < 0 || max_seqlen_q < 0) return fail(VOX_EINVAL, "prefill_attn: negative batch or max_seqlen_q");
   if (batch == 0 || max_seqlen_q == 0) return VOX_OK;
-  if (!q || !out) return fail(VOX_EINVAL, "prefill_attn: null q or out");
-  if (head_dim != kHeadDim) return fail(VOX_EINVAL, "prefill_attn: head_dim %d unsupported (128 only)", head_dim);
-  if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads)
-    return fail(VOX_EINVAL, "prefill_attn: num_heads %d not a multiple of num_kv_heads %d", num_heads,
-                num_kv_heads);
-  const int group = num_heads / num_kv_heads;
-  if (128 % group) return fail(VOX_EINVAL, "prefill_attn: group size %d must divide 128", group);
-  if ((cu_seqlens_q == nullptr) != (cu_seqlens_k == nullptr))
-    return fail(VOX_EINVAL, "prefill_attn: give both cu_seqlens or neither");
-  if (!cu_seqlens_q && (uniform_seqlen_q <= 0 || uniform_seqlen_k <= 0))
-    return fail(VOX_EINVAL, "prefill_attn: uniform lengths must be positive without cu_seqlens");
-  if (!cu_seqlens_q && max_seqlen_q != uniform_seqlen_q)
-    return fail(VOX_EINVAL, "prefill_attn: max_seqlen_q must equal the uniform length");
-  if (q_row_stride < (int64_t)num_heads * head_dim || q_row_stride % 8 || !aligned16(q))
-    return fail(VOX_EINVAL, "prefill_attn: q must be 16-byte aligned with a row stride >= H*D, multiple of 8");
+  if (!out) return fail(VOX_EINVAL, "prefill_attn: null out");
   if (out_row_stride < (int64_t)num_heads * head_dim || out_row_stride % 4 || ((uintptr_t)out & 7u))
     return fail(VOX_EINVAL, "prefill_attn: bad out row stride or alignment");
-  if (!std::isfinite(softmax_scale)) return fail(VOX_EINVAL, "prefill_attn: softmax_scale is not finite");
-  if (block_tables) {
-    if (!k_cache || !v_cache) return fail(VOX_EINVAL, "prefill_attn: block tables without caches");
-    if (block_size <= 0 || max_blocks <= 0 || bt_stride < max_blocks || num_blocks <= 0)
-      return fail(VOX_EINVAL, "prefill_attn: bad block table or cache shape");
-    if (!aligned16(k_cache) || !aligned16(v_cache)) return fail(VOX_EINVAL, "prefill_attn: caches not aligned");
-  } else {
-    if (!key || !value) return fail(VOX_EINVAL, "prefill_attn: null key/value without block tables");
-    if (key_row_stride < (int64_t)num_kv_heads * head_dim || value_row_stride < (int64_t)num_kv_heads * head_dim ||
-        key_row_stride % 8 || value_row_stride % 8 || !aligned16(key) || !aligned16(value))
-      return fail(VOX_EINVAL, "prefill_attn: key/value must be 16-byte aligned rows, stride multiple of 8");
-  }
-
   vox::PrefillArgs a;
-  a.q = (const uint16_t*)q;
-  a.q_row_stride = q_row_stride;
-  a.k_src = (const uint16_t*)key;
-  a.v_src = (const uint16_t*)value;
-  a.k_row_stride = key_row_stride;
-  a.v_row_stride = value_row_stride;
-  a.k_cache = (const uint16_t*)k_cache;
-  a.v_cache = (const uint16_t*)v_cache;
-  a.num_blocks = num_blocks;
-  a.block_size = block_size;
-  a.block_tables = block_tables;
-  a.bt_stride = bt_stride;
-  a.max_blocks = max_blocks;
-  a.cu_q = cu_seqlens_q;
-  a.cu_k = cu_seqlens_k;
-  a.uniform_q = uniform_seqlen_q;
-  a.uniform_k = uniform_seqlen_k;
-  a.batch = batch;
-  a.num_heads = num_heads;
-  a.num_kv_heads = num_kv_heads;
-  a.group = group;
-  a.scale_log2 = softmax_scale * 1.4426950408889634f;
-  a.causal = causal ? 1 : 0;
+  const int st = prefill_setup("prefill_attn", q, q_row_stride, key, value, key_row_stride, value_row_stride, k_cache,
+                               v_cache, num_blocks, block_size, block_tables, bt_stride, max_blocks, cu_seqlens_q,
+                               cu_seqlens_k, batch, max_seqlen_q, uniform_seqlen_q, uniform_seqlen_k, num_heads,
+                               num_kv_heads, head_dim, softmax_scale, causal, &a);
+  if (st != VOX_OK) return st;
   a.out = (uint16_t*)out;
   a.out_row_stride = out_row_stride;
   return hip_status(vox::launch_prefill(a, max_seqlen_q, (hipStream_t)stream), "prefill_attn launch");
+}
+
+int vox_prefill_attn_int8(const void* q, int64_t q_row_stride, const void* key, const void* value,
+                          int64_t key_row_stride, int64_t value_row_stride, const void* k_cache, const void* v_cache,
+                          int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
+                          int max_blocks, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch,
+                          int max_seqlen_q, int uniform_seqlen_q, int uniform_seqlen_k, int num_heads,
+                          int num_kv_heads, int head_dim, float softmax_scale, int causal, const float* inv_smooth,
+                          void* out_q, int64_t out_q_row_stride, float* out_scale, void* stream) {
+  if (batch < 0 || max_seqlen_q < 0) return fail(VOX_EINVAL, "prefill_attn_int8: negative batch or max_seqlen_q");
+  if (batch == 0 || max_seqlen_q == 0) return VOX_OK;
+  if (!out_q || !out_scale) return fail(VOX_EINVAL, "prefill_attn_int8: null out_q or out_scale");
+  if (num_kv_heads != 1 && num_kv_heads != 2)
+    return fail(VOX_EINVAL, "prefill_attn_int8: num_kv_heads %d unsupported (1 or 2)", num_kv_heads);
+  if (out_q_row_stride < (int64_t)num_heads * head_dim || out_q_row_stride % 4 || ((uintptr_t)out_q & 3u))
+    return fail(VOX_EINVAL, "prefill_attn_int8: bad out_q row stride or alignment");
+  if (((uintptr_t)out_scale & 3u) || (inv_smooth && !aligned16(inv_smooth)))
+    return fail(VOX_EINVAL, "prefill_attn_int8: out_scale must be 4-byte and inv_smooth 16-byte aligned");
+  vox::PrefillArgs a;
+  const int st = prefill_setup("prefill_attn_int8", q, q_row_stride, key, value, key_row_stride, value_row_stride,
+                               k_cache, v_cache, num_blocks, block_size, block_tables, bt_stride, max_blocks,
+                               cu_seqlens_q, cu_seqlens_k, batch, max_seqlen_q, uniform_seqlen_q, uniform_seqlen_k,
+                               num_heads, num_kv_heads, head_dim, softmax_scale, causal, &a);
+  if (st != VOX_OK) return st;
+  a.inv_smooth = inv_smooth;
+  a.out_q = (int8_t*)out_q;
+  a.out_row_stride = out_q_row_stride;
+  a.out_scale = out_scale;
+  return hip_status(vox::launch_prefill_int8(a, max_seqlen_q, (hipStream_t)stream), "prefill_attn_int8 launch");
 }
 
 }  // extern "C"

@@ -12,6 +12,13 @@
 // row-major and V transposed ([d][key]) in LDS; each wave computes S^T[64 keys x 32 rows] = K Q^T with Q^T held in
 // registers, an online softmax in fp32 (exp2, log2-prescaled scale), and O^T[128 d x 32 rows] += V^T P^T, where P^T
 // comes out of the score MFMA already in B-operand layout.
+//
+// int8 output (QUANT; reference: the QUANT epilogues of kernels/prefill_attn.py:84-92 and kernels/short_attn.py:
+// 55-64, 137-146): the o_proj GEMM takes o per token as int8 plus one fp32 scale over all heads, so a workgroup then
+// holds the same query tokens for every KV group (one 4-wave half per group, each with its own K/V tiles; the
+// halves step through the key tiles together). The epilogue multiplies the normalized fp32 o by inv_smooth, takes
+// the per-token max |.| across both halves (LDS atomic max on the float bits, all values >= 0), and writes
+// rint(o / scale) (round half to even) with scale = max(amax, 1e-6) / 127.
 #include "vox_common.h"
 #include "vox_kernels.h"
 
@@ -25,13 +32,19 @@ constexpr int kRows = 128;       // query rows per workgroup
 constexpr int kKsStride = kD + 8;   // LDS K row: 128 d + 8 pad (bf16)
 constexpr int kVtStride = kBK + 8;  // LDS V^T row: 64 keys + 8 pad (bf16)
 
-__global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs p) {
-  __shared__ __attribute__((aligned(16))) uint16_t ks[kBK][kKsStride];
-  __shared__ __attribute__((aligned(16))) uint16_t vts[kD][kVtStride];
+template <bool QUANT>
+__global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kernel(PrefillArgs p) {
+  constexpr int NH = QUANT ? 2 : 1;  // KV-group halves per workgroup
+  __shared__ __attribute__((aligned(16))) uint16_t ks_all[NH][kBK][kKsStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vts_all[NH][kD][kVtStride];
+  __shared__ unsigned s_amax[QUANT ? kRows : 1];  // QUANT: per token of the tile, float bits of max |o|
 
   const int qt = blockIdx.x;
   const int b = blockIdx.y;
-  const int g = blockIdx.z;
+  const int half = QUANT ? (int)(threadIdx.x >> 8) : 0;
+  const int g = QUANT ? half : (int)blockIdx.z;
+  auto& ks = ks_all[half];
+  auto& vts = vts_all[half];
   int q0, nq, k0, nk;
   if (p.cu_q) {
     q0 = p.cu_q[b];
@@ -52,8 +65,10 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs p) {
   const int BQ = kRows / G;  // query tokens per workgroup
   if (qt * BQ >= nq) return;
 
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x & 255;  // thread within the half
   const int w = tid >> 6;
+  if constexpr (QUANT)
+    if (threadIdx.x < (unsigned)BQ) s_amax[threadIdx.x] = 0u;  // ordered before the atomics by the barriers below
   const int lane = tid & 63;
   const int r16 = lane & 15;
   const int jq = lane >> 4;
@@ -199,6 +214,47 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs p) {
     __syncthreads();
   }
 
+  if constexpr (QUANT) {
+    // ---- int8 epilogue: o * inv_smooth, per-token amax over all heads, rint(o / scale) ----
+    const int g_rows = G;
+    float lmax[2] = {0.f, 0.f};
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const float L = col_sum4(l[rt]);
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        f32x4 o = acc[dt][rt] * inv;
+        if (p.inv_smooth) o *= *reinterpret_cast<const f32x4*>(p.inv_smooth + h_of[rt] * kD + dt * 16 + jq * 4);
+        acc[dt][rt] = o;
+        lmax[rt] = fmaxf(lmax[rt], fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3]))));
+      }
+    }
+    __syncthreads();  // s_amax cleared (also when no key tile ran)
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+      if (row_ok[rt]) atomicMax(&s_amax[(w * 32 + rt * 16 + r16) / g_rows], __float_as_uint(lmax[rt]));
+    __syncthreads();
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      if (!row_ok[rt]) continue;
+      const float scale = fmaxf(__uint_as_float(s_amax[(w * 32 + rt * 16 + r16) / g_rows]), 1e-6f) / 127.f;
+      int8_t* op = p.out_q + (int64_t)(q0 + tq_of[rt]) * p.out_row_stride + (int64_t)h_of[rt] * kD + jq * 4;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const f32x4 o = acc[dt][rt];
+        uint32_t packed = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          packed |= (uint32_t)(uint8_t)(int8_t)(int)__builtin_rintf(o[e] / scale) << (8 * e);
+        *reinterpret_cast<uint32_t*>(op + dt * 16) = packed;
+      }
+    }
+    if (threadIdx.x < (unsigned)BQ && qt * BQ + (int)threadIdx.x < nq)
+      p.out_scale[q0 + qt * BQ + threadIdx.x] = fmaxf(__uint_as_float(s_amax[threadIdx.x]), 1e-6f) / 127.f;
+    return;
+  }
+
   // ---- epilogue: normalize, bf16, 4 consecutive dims per lane per d-tile ----
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
@@ -222,7 +278,17 @@ hipError_t launch_prefill(const PrefillArgs& a, int max_seqlen_q, hipStream_t st
   const int q_tiles = (max_seqlen_q + bq - 1) / bq;
   if (q_tiles <= 0 || a.batch <= 0) return hipSuccess;
   dim3 grid((unsigned)q_tiles, (unsigned)a.batch, (unsigned)a.num_kv_heads);
-  prefill_kernel<<<grid, dim3(256), 0, stream>>>(a);
+  prefill_kernel<false><<<grid, dim3(256), 0, stream>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill_int8(const PrefillArgs& a, int max_seqlen_q, hipStream_t stream) {
+  const int bq = kRows / a.group;
+  const int q_tiles = (max_seqlen_q + bq - 1) / bq;
+  if (q_tiles <= 0 || a.batch <= 0) return hipSuccess;
+  if (a.num_kv_heads < 1 || a.num_kv_heads > 2) return hipErrorInvalidValue;
+  dim3 grid((unsigned)q_tiles, (unsigned)a.batch, 1u);
+  prefill_kernel<true><<<grid, dim3(256 * a.num_kv_heads), 0, stream>>>(a);
   return hipGetLastError();
 }
 

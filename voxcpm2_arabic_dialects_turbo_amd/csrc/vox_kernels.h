@@ -63,6 +63,11 @@ struct PrefillArgs {
   int causal;                 // bottom-right aligned: query i of nq sees keys j <= nk - nq + i
   uint16_t* out;              // bf16 [T, H, 128]; token rows out_row_stride apart
   int64_t out_row_stride;
+  // int8 output (launch_prefill_int8): per token, o * inv_smooth (inv_smooth fp32 [H * 128] or null) over all
+  // heads -> amax; out_q = rint(o * inv_smooth / scale) with scale = max(amax, 1e-6) / 127, out_scale[token] = scale
+  const float* inv_smooth;
+  int8_t* out_q;              // int8 [T, H * 128]; token rows out_row_stride apart
+  float* out_scale;           // fp32 [T]
 };
 
 hipError_t launch_store_kvcache(const void* k, const void* v, int64_t k_row_stride, int64_t v_row_stride,
@@ -72,5 +77,8 @@ hipError_t launch_store_kvcache(const void* k, const void* v, int64_t k_row_stri
 hipError_t launch_decode(const DecodeArgs& a, int num_kv_heads, hipStream_t stream);
 
 hipError_t launch_prefill(const PrefillArgs& a, int max_seqlen_q, hipStream_t stream);
+
+// The same attention with the int8 epilogue; one workgroup covers every KV group of its tokens (num_kv_heads <= 2).
+hipError_t launch_prefill_int8(const PrefillArgs& a, int max_seqlen_q, hipStream_t stream);
 
 }  // namespace vox

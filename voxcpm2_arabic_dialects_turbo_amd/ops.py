@@ -128,18 +128,29 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor | None, v: torch.Tensor | 
                      softmax_scale: float, causal: bool, block_table: torch.Tensor | None = None,
                      k_cache: torch.Tensor | None = None, v_cache: torch.Tensor | None = None,
                      batch: int | None = None, uniform_seqlen_q: int = 0, uniform_seqlen_k: int = 0,
-                     out: torch.Tensor | None = None) -> torch.Tensor:
+                     out: torch.Tensor | None = None, quant: bool = False, inv_smooth: torch.Tensor | None = None):
     """The varlen prefill kernel. q [T, H, 128] (token rows may be strided). K/V from packed rows k / v
     [Tk, HK, 128] or, with block_table, from k_cache / v_cache [num_blocks, block_size, HK, 128]. Sequences from
     cu_seqlens_q / cu_seqlens_k (int32 [B + 1]) or, when both are None, `batch` sequences of uniform lengths.
-    Returns o [T, H, 128] bf16."""
+    Returns o [T, H, 128] bf16; with ``quant`` (HK <= 2), (int8 o [T, H * 128], fp32 scale [T]): per token
+    o * inv_smooth (fp32 [H * 128], optional) over all heads quantized to rint(o / scale), scale = max(amax, 1e-6) / 127
+    (reference: the QUANT epilogues of kernels/prefill_attn.py:84-92, kernels/short_attn.py:55-64, 137-146)."""
     T, H, D = q.shape
     dev = _check_cuda(q)
     if q.dtype != torch.bfloat16:
         raise TypeError("varlen attention takes bf16 q")
     if D != HEAD_DIM or q.stride(2) != 1 or q.stride(1) != D:
         raise ValueError(f"q must be [T, H, {HEAD_DIM}] with contiguous heads, got {tuple(q.shape)} {q.stride()}")
-    if out is None:
+    if quant:
+        out_q = torch.empty(T, H * D, dtype=torch.int8, device=dev)
+        out_scale = torch.empty(T, dtype=torch.float32, device=dev)
+        if inv_smooth is not None:
+            _check_cuda(q, inv_smooth)
+            if inv_smooth.numel() != H * D:
+                raise ValueError(f"inv_smooth must hold H * head_dim = {H * D} values")
+            inv_smooth = inv_smooth.reshape(-1).to(torch.float32).contiguous()
+        out = (out_q, out_scale)
+    elif out is None:
         out = torch.empty(T, H, D, dtype=q.dtype, device=dev)
     if cu_seqlens_q is not None:
         B = cu_seqlens_q.numel() - 1
@@ -183,6 +194,17 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor | None, v: torch.Tensor | 
         args = (k.data_ptr(), v.data_ptr(), k.stride(0), v.stride(0), 0, 0, 0, 0, 0, 0, 0)
     if H % HK:
         raise ValueError(f"num_heads {H} is not a multiple of num_kv_heads {HK}")
+    if quant:
+        _lib.check(lib.vox_prefill_attn_int8(q.data_ptr(), q.stride(0), *args,
+                                             None if cu_q is None else cu_q.data_ptr(),
+                                             None if cu_k is None else cu_k.data_ptr(), B, int(max_seqlen_q),
+                                             int(uniform_seqlen_q), int(uniform_seqlen_k), H, HK, D,
+                                             float(softmax_scale), 1 if causal else 0,
+                                             None if inv_smooth is None else inv_smooth.data_ptr(),
+                                             out_q.data_ptr(), out_q.stride(0), out_scale.data_ptr(),
+                                             _lib.stream_handle(dev)),
+                   "prefill_attn_int8")
+        return out
     _lib.check(lib.vox_prefill_attn(q.data_ptr(), q.stride(0), *args,
                                     None if cu_q is None else cu_q.data_ptr(),
                                     None if cu_k is None else cu_k.data_ptr(), B, int(max_seqlen_q),
