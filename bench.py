@@ -254,6 +254,35 @@ def bench_prefill(dev):
     return out
 
 
+def bench_kv_copy(dev):
+    """copy_kv_block_prefix over the model's cache layout (36 causal layers x K/V, 256-slot blocks): the voice-cloning
+    prefix copy (44 entries x 50 tokens) and full-block copies (64 entries x 256 tokens); GB/s of bytes read and
+    written."""
+    import torch
+
+    from voxcpm2_arabic_dialects_turbo_amd import _lib
+
+    lib = _lib.load()
+    blocks = 160
+    kv = torch.empty(36, 2, blocks, BS, HK, D, dtype=torch.bfloat16, device=dev)
+    kv.view(-1)[:] = 1
+    out = {}
+    perm = torch.randperm(blocks, generator=torch.Generator().manual_seed(53)).tolist()
+    for name, n_entries, n_tok in (("prefix_44x50", 44, 50), ("full_64x256", 64, 256)):
+        # the entries table is uploaded once (the wrapper's per-call pinned upload is not graph-capturable)
+        pairs = torch.tensor([(perm[2 * i], perm[2 * i + 1], n_tok) for i in range(n_entries)], dtype=torch.int32,
+                             device=dev)
+
+        def run(pairs=pairs, n_entries=n_entries, n_tok=n_tok):
+            _lib.check(lib.vox_copy_kv_block_prefix(kv.data_ptr(), 72, blocks, BS, HK * D, 2, pairs.data_ptr(),
+                                                    n_entries, n_tok, _lib.stream_handle(dev)), "copy")
+
+        ms = _graph_ms(run, 20)
+        nbytes = 2 * n_entries * 72 * n_tok * HK * D * 2
+        out[name] = dict(launch_us=round(ms * 1e3, 2), bytes=nbytes, gbs=round(nbytes / (ms * 1e-3) / 1e9, 1))
+    return out
+
+
 def cpu_baseline(w, budget_s: float):
     """The oracle's torch path (fp32, as the reference's tests compute it) on the host cores over a bounded sample of
     the same decode step: layer after layer (store + decode of 150 sequences) until the budget is spent."""
@@ -358,6 +387,7 @@ def main():
     }
     if not args.decode_only:
         line["prefill"] = bench_prefill(dev)
+        line["kv_block_prefix_copy"] = bench_kv_copy(dev)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(res["workload"], args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define VOX_ABI_VERSION 4
+#define VOX_ABI_VERSION 5
 
 #define VOX_OK 0
 #define VOX_EINVAL 1 /* bad argument: shape, stride, alignment or null pointer (reference: the asserts of
@@ -101,6 +101,19 @@ int vox_prefill_attn_int8(const void* q, int64_t q_row_stride, const void* key, 
                           int max_seqlen_q, int uniform_seqlen_q, int uniform_seqlen_k, int num_heads,
                           int num_kv_heads, int head_dim, float softmax_scale, int causal, const float* inv_smooth,
                           void* out_q, int64_t out_q_row_stride, float* out_scale, void* stream);
+
+/* Copy the first n token slots of KV-cache blocks in every (layer, K/V) plane, in one launch. Replaces
+ * copy_kv_block_prefix (reference: nanovllm_voxcpm/kernels/kv_copy.py:17-41; callers model/runner.py:232-248,
+ * model/engine.py:383-452).
+ *   kv          2-byte elements [num_planes, num_blocks, block_size, per_token], contiguous (the engine's
+ *               [layers, 2, blocks, block_size, kv_heads, head_dim] tensor: num_planes = layers * 2,
+ *               per_token = kv_heads * head_dim)
+ *   entries     device int32 [num_entries, 3]: (src block, dst block, n tokens); n is clipped to block_size and
+ *               n <= 0 does nothing; entries with a block outside [0, num_blocks) are skipped
+ *   max_tokens  an upper bound of the entries' n (sizes the launch; host-known, as the reference's grid)
+ * Bit-exact. Entries that write a block another entry of the same call reads race, as in the reference. */
+int vox_copy_kv_block_prefix(void* kv, int64_t num_planes, int64_t num_blocks, int block_size, int64_t per_token,
+                             int elem_bytes, const int32_t* entries, int num_entries, int max_tokens, void* stream);
 
 #ifdef __cplusplus
 }

@@ -141,6 +141,28 @@ def test_prefill_int8_rejects_bad_arguments():
     assert lib.vox_prefill_attn_int8(*zero) == _lib.VOX_OK
 
 
+def test_copy_kv_block_prefix_rejects_bad_arguments():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    args = [p, 72, 64, 256, 256, 2, p, 3, 256, None]  # valid apart from the fake pointers: never passed unmodified
+    bad = list(args)
+    bad[5] = 4  # 4-byte elements
+    assert lib.vox_copy_kv_block_prefix(*bad) == _lib.VOX_EINVAL and "2 only" in _err()
+    bad = list(args)
+    bad[0] = None
+    assert lib.vox_copy_kv_block_prefix(*bad) == _lib.VOX_EINVAL and "null" in _err()
+    bad = list(args)
+    bad[1] = 70000
+    assert lib.vox_copy_kv_block_prefix(*bad) == _lib.VOX_EINVAL and "planes" in _err()
+    bad = list(args)
+    bad[3] = 0
+    assert lib.vox_copy_kv_block_prefix(*bad) == _lib.VOX_EINVAL and "shape" in _err()
+    for i, v in ((7, 0), (8, 0), (1, 0)):  # nothing to copy: no launch
+        ok = list(args)
+        ok[i] = v
+        assert lib.vox_copy_kv_block_prefix(*ok) == _lib.VOX_OK
+
+
 def test_python_errors_carry_the_library_message():
     with pytest.raises(ValueError, match="head_dim"):
         _lib.check(_decode(d=64), "decode_attn")

@@ -236,3 +236,17 @@ def test_reference_kernel_mirrors_keep_their_contracts():
     cache = torch.zeros(2, 256, 2, 128, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="GPU"):
         paged_prefill_attention(q, cache, cache, torch.zeros(1, 1, dtype=torch.int32), cu, cu, 3, 0.1, quant=True)
+
+
+def test_copy_kv_block_prefix_keeps_the_reference_contract():
+    """Entries with n <= 0 are dropped before anything else (no call at all); a non-contiguous cache fails the
+    reference's assert; a CPU cache with work to do is rejected (no CPU fallback)."""
+    from voxcpm2_arabic_dialects_turbo_amd.kernels.kv_copy import copy_kv_block_prefix
+
+    kv = torch.zeros(2, 2, 4, 16, 2, 128, dtype=torch.bfloat16)
+    copy_kv_block_prefix(kv, [(0, 1, 0), (2, 3, -5)])
+    copy_kv_block_prefix(kv, [])
+    with pytest.raises(AssertionError):
+        copy_kv_block_prefix(kv.transpose(0, 1), [(0, 1, 3)])
+    with pytest.raises(ValueError, match="GPU"):
+        copy_kv_block_prefix(kv, [(0, 1, 3)])

@@ -298,3 +298,26 @@ def test_quantize_rows_matches_an_elementwise_loop():
         # the reference test's bound on the dequantized row (tests/test_kernel_references.py:206-209)
         err = (ref.dequantize_rows(q[i:i + 1], scale[i:i + 1]) - x[i:i + 1] * inv).abs()
         assert bool((err <= 0.51 * scale[i]).all())
+
+
+# --- KV block-prefix copy --------------------------------------------------------------------------------------------
+
+def test_kv_block_prefix_copy_known_answer():
+    """Every element holds its own flat index, so each copied run is identified exactly: block dst's first n slots of
+    every (layer, K/V) plane equal block src's, everything else is untouched; n is clipped to the block size and
+    n <= 0 does nothing (reference: kernels/kv_copy.py:31-35)."""
+    from oracle import kvcopy
+
+    kv = torch.arange(3 * 2 * 5 * 4 * 2 * 3, dtype=torch.float64).reshape(3, 2, 5, 4, 2, 3)
+    orig = kv.clone()
+    kvcopy.copy_kv_block_prefix(kv, [(1, 3, 2), (0, 4, 9), (2, 2, 0), (3, 0, -1)])
+    want = orig.clone()
+    want[:, :, 3, :2] = orig[:, :, 1, :2]
+    want[:, :, 4, :4] = orig[:, :, 0, :4]  # 9 clipped to the block size
+    assert torch.equal(kv, want)
+    # the flat formula of the reference's kernel: plane p, element o of the run -> p*plane + block*bstride + o
+    flat, oflat = kv.reshape(6, -1), orig.reshape(6, -1)
+    bstride = 4 * 2 * 3
+    for p in range(6):
+        for o in range(2 * 2 * 3):
+            assert flat[p, 3 * bstride + o] == oflat[p, 1 * bstride + o]

@@ -19,7 +19,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_NAME = "libvoxattn.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["store_kvcache.hip", "decode_attn.hip", "prefill_attn.hip", "capi.hip"]
+SOURCES = ["store_kvcache.hip", "decode_attn.hip", "prefill_attn.hip", "kv_copy.hip", "capi.hip"]
 ARCH = "gfx950"
 
 

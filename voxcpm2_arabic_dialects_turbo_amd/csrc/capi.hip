@@ -271,4 +271,28 @@ int vox_prefill_attn_int8(const void* q, int64_t q_row_stride, const void* key, 
   return hip_status(vox::launch_prefill_int8(a, max_seqlen_q, (hipStream_t)stream), "prefill_attn_int8 launch");
 }
 
+int vox_copy_kv_block_prefix(void* kv, int64_t num_planes, int64_t num_blocks, int block_size,
+                              int64_t per_token, int elem_bytes, const int32_t* entries, int num_entries,
+                              int max_tokens, void* stream) {
+  if (num_entries < 0 || num_planes < 0) return fail(VOX_EINVAL, "copy_kv_block_prefix: negative count");
+  if (num_entries == 0 || num_planes == 0 || max_tokens <= 0) return VOX_OK;
+  if (!kv || !entries) return fail(VOX_EINVAL, "copy_kv_block_prefix: null kv or entries");
+  if (elem_bytes != 2) return fail(VOX_EINVAL, "copy_kv_block_prefix: %d-byte elements unsupported (2 only)", elem_bytes);
+  if (num_blocks <= 0 || block_size <= 0 || per_token <= 0)
+    return fail(VOX_EINVAL, "copy_kv_block_prefix: bad cache shape");
+  if (num_planes > 65535) return fail(VOX_EINVAL, "copy_kv_block_prefix: more than 65535 planes");
+  if (max_tokens > block_size) max_tokens = block_size;
+  vox::CopyArgs a;
+  a.kv = kv;
+  a.num_planes = num_planes;
+  a.num_blocks = num_blocks;
+  a.block_size = block_size;
+  a.per_token = per_token;
+  a.entries = entries;
+  a.num_entries = num_entries;
+  const bool vec16 = per_token % 8 == 0 && aligned16(kv);
+  return hip_status(vox::launch_copy_block_prefix(a, max_tokens, vec16, (hipStream_t)stream),
+                    "copy_kv_block_prefix launch");
+}
+
 }  // extern "C"

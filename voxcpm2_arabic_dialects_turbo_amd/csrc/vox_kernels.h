@@ -70,6 +70,16 @@ struct PrefillArgs {
   float* out_scale;           // fp32 [T]
 };
 
+struct CopyArgs {
+  void* kv;                   // [num_planes][num_blocks][block_size][per_token] elements, contiguous
+  int64_t num_planes;         // layers x 2 (K, V)
+  int64_t num_blocks;
+  int block_size;
+  int64_t per_token;          // elements per token slot (kv_heads x head_dim)
+  const int32_t* entries;     // int32 [num_entries][3]: src block, dst block, tokens
+  int num_entries;
+};
+
 hipError_t launch_store_kvcache(const void* k, const void* v, int64_t k_row_stride, int64_t v_row_stride,
                                 void* k_cache, void* v_cache, int64_t num_slots, const int32_t* slot_mapping,
                                 int64_t n, int row_elems, bool vec16, hipStream_t stream);
@@ -77,6 +87,8 @@ hipError_t launch_store_kvcache(const void* k, const void* v, int64_t k_row_stri
 hipError_t launch_decode(const DecodeArgs& a, int num_kv_heads, hipStream_t stream);
 
 hipError_t launch_prefill(const PrefillArgs& a, int max_seqlen_q, hipStream_t stream);
+
+hipError_t launch_copy_block_prefix(const CopyArgs& a, int max_tokens, bool vec16, hipStream_t stream);
 
 // The same attention with the int8 epilogue; one workgroup covers every KV group of its tokens (num_kv_heads <= 2).
 hipError_t launch_prefill_int8(const PrefillArgs& a, int max_seqlen_q, hipStream_t stream);
