@@ -40,17 +40,8 @@ constexpr int kThreads = kWaves * kWave;
 constexpr int kStep = kWaves * kTile;  // tokens per workgroup step
 constexpr int kMaxHeads = 16;
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-
 __device__ __forceinline__ f32x4 mfma_16x16x16(s16x4 a, s16x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
-}
-
-// Transposed LDS read: within each 16-lane group, lane j returns element j%4 of the 8-byte chunks that lanes
-// 4r + j/4 (r = 0..3) address, i.e. four rows of one column when lanes 4r + q point at row r, column 4q.
-__device__ __forceinline__ s16x4 lds_read_tr16(const uint16_t* p) {
-  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
 }
 
 template <int HK>

@@ -8,10 +8,14 @@
 // paged cache through block_tables, or from packed [Tk, HK, D] rows when there is no block table.
 //
 // gfx950 mapping. A workgroup (4 waves, 256 threads) owns 128 query rows = (128 / G tokens) x (the G query heads of
-// one kv head): GQA shares every K/V tile across the group's heads. Per 64-key tile the workgroup stages K
-// row-major and V transposed ([d][key]) in LDS; each wave computes S^T[64 keys x 32 rows] = K Q^T with Q^T held in
-// registers, an online softmax in fp32 (exp2, log2-prescaled scale), and O^T[128 d x 32 rows] += V^T P^T, where P^T
-// comes out of the score MFMA already in B-operand layout.
+// one kv head): GQA shares every K/V tile across the group's heads. Per 64-key tile the workgroup stages K and V
+// row-major in LDS (16-byte stores); each wave computes S^T[64 keys x 32 rows] = K Q^T with Q^T held in registers,
+// an online softmax in fp32 (exp2, log2-prescaled scale), and O^T[128 d x 32 rows] += V^T P^T, where P^T comes out of
+// the score MFMA already in B-operand layout and V^T is read with ds_read_b64_tr_b16 (two transposed reads give a
+// lane the 8 keys of one d column). The next tile's K/V loads are issued into registers before the current tile is
+// computed, so their latency hides behind the MFMA work; in paged mode the block ids are read one tile further
+// ahead, so a tile's loads never wait on a lookup. The causal / length mask is only evaluated on tiles that reach
+// past the first query's position or past the keys.
 //
 // int8 output (QUANT; reference: the QUANT epilogues of kernels/prefill_attn.py:84-92 and kernels/short_attn.py:
 // 55-64, 137-146): the o_proj GEMM takes o per token as int8 plus one fp32 scale over all heads, so a workgroup then
@@ -29,14 +33,14 @@ namespace {
 constexpr int kD = 128;
 constexpr int kBK = 64;          // keys per tile
 constexpr int kRows = 128;       // query rows per workgroup
-constexpr int kKsStride = kD + 8;   // LDS K row: 128 d + 8 pad (bf16)
-constexpr int kVtStride = kBK + 8;  // LDS V^T row: 64 keys + 8 pad (bf16)
+constexpr int kKsStride = kD + 8;   // LDS K / V row: 128 d + 8 pad (bf16); 16 consecutive rows of a transposed
+                                    // read then cover every bank exactly twice
 
 template <bool QUANT>
 __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kernel(PrefillArgs p) {
   constexpr int NH = QUANT ? 2 : 1;  // KV-group halves per workgroup
   __shared__ __attribute__((aligned(16))) uint16_t ks_all[NH][kBK][kKsStride];
-  __shared__ __attribute__((aligned(16))) uint16_t vts_all[NH][kD][kVtStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vs_all[NH][kBK][kKsStride];
   __shared__ unsigned s_amax[QUANT ? kRows : 1];  // QUANT: per token of the tile, float bits of max |o|
 
   const int qt = blockIdx.x;
@@ -44,7 +48,7 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
   const int half = QUANT ? (int)(threadIdx.x >> 8) : 0;
   const int g = QUANT ? half : (int)blockIdx.z;
   auto& ks = ks_all[half];
-  auto& vts = vts_all[half];
+  auto& vs = vs_all[half];
   int q0, nq, k0, nk;
   if (p.cu_q) {
     q0 = p.cu_q[b];
@@ -105,43 +109,72 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) acc[dt][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int kv0 = 0; kv0 < kv_end; kv0 += kBK) {
-    // ---- stage the K (row-major) and V (transposed) tiles of kv head g ----
+  // ---- K/V tile loads: 4 + 4 pieces of 16 bytes per thread (key kk = pc / 16, dims dc .. dc + 8), unconditional
+  // and in bounds (a key past nk or in an unmapped block reads a valid address and is zeroed when staged). In paged
+  // mode the pieces' block ids are read one tile ahead (fetch_bids), so a tile's eight loads issue back to back
+  // instead of each waiting on its own lookup.
+  u32x4 kr[4], vr[4];
+  int bids[4] = {0, 0, 0, 0};
+  unsigned live = 0;  // bit i: piece i is a real key
+  auto fetch_bids = [&](int kv0) {
+    if (!p.block_tables) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int jc = min(kv0 + (tid >> 4) + 16 * i, nk - 1);
+      bids[i] = p.block_tables[(int64_t)b * p.bt_stride + jc / p.block_size];
+    }
+  };
+  auto load_tile = [&](int kv0) {
+    live = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int pc = tid + i * 256;
-      const int kk = pc >> 4;
       const int dc = (pc & 15) * 8;
-      const int jj = kv0 + kk;
-      u32x4 kv = zero4(), vv = zero4();
-      if (jj < nk) {
-        const uint16_t* kp = nullptr;
-        const uint16_t* vp = nullptr;
-        if (p.block_tables) {
-          const int col = jj / p.block_size;
-          const int64_t blk = p.block_tables[(int64_t)b * p.bt_stride + col];
-          if (blk >= 0 && blk < p.num_blocks) {
-            const int64_t off = ((blk * p.block_size + jj % p.block_size) * HK + g) * kD + dc;
-            kp = p.k_cache + off;
-            vp = p.v_cache + off;
-          }
-        } else {
-          kp = p.k_src + (int64_t)(k0 + jj) * p.k_row_stride + g * kD + dc;
-          vp = p.v_src + (int64_t)(k0 + jj) * p.v_row_stride + g * kD + dc;
-        }
-        if (kp) {
-          kv = ld_g16(kp);
-          vv = ld_g16(vp);
-        }
+      const int jj = kv0 + (pc >> 4);
+      const int jc = min(jj, nk - 1);
+      const uint16_t* kp;
+      const uint16_t* vp;
+      bool ok = jj < nk;
+      if (p.block_tables) {
+        const int64_t blk = bids[i];
+        ok = ok && blk >= 0 && blk < p.num_blocks;
+        const int64_t off = (((ok ? blk : 0) * p.block_size + jc % p.block_size) * HK + g) * kD + dc;
+        kp = p.k_cache + off;
+        vp = p.v_cache + off;
+      } else {
+        kp = p.k_src + (int64_t)(k0 + jc) * p.k_row_stride + g * kD + dc;
+        vp = p.v_src + (int64_t)(k0 + jc) * p.v_row_stride + g * kD + dc;
       }
-      *reinterpret_cast<u32x4*>(&ks[kk][dc]) = kv;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vts[dc + 2 * e][kk] = (uint16_t)(vv[e] & 0xffffu);
-        vts[dc + 2 * e + 1][kk] = (uint16_t)(vv[e] >> 16);
-      }
+      kr[i] = ld_g16(kp);
+      vr[i] = ld_g16(vp);
+      live |= (ok ? 1u : 0u) << i;
     }
+  };
+  auto stage_tile = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int pc = tid + i * 256;
+      const bool ok = (live >> i) & 1u;
+      *reinterpret_cast<u32x4*>(&ks[pc >> 4][(pc & 15) * 8]) = ok ? kr[i] : zero4();
+      *reinterpret_cast<u32x4*>(&vs[pc >> 4][(pc & 15) * 8]) = ok ? vr[i] : zero4();
+    }
+  };
+  // this lane's transposed-read address inside a 16-key x 16-d block: row jq*4 + r16/4, column 4*(r16%4)
+  const int tr_off = (jq * 4 + (r16 >> 2)) * kKsStride + 4 * (r16 & 3);
+  const int first_pos = nk - nq + qt * BQ;  // the position of the tile's first query token
+
+  if (kv_end > 0) {
+    fetch_bids(0);
+    load_tile(0);
+    fetch_bids(kBK);
+  }
+  for (int kv0 = 0; kv0 < kv_end; kv0 += kBK) {
+    stage_tile();
     __syncthreads();
+    if (kv0 + kBK < kv_end) {  // in flight while this tile computes
+      load_tile(kv0 + kBK);
+      fetch_bids(kv0 + 2 * kBK);
+    }
 
     // ---- S^T[key][row] = K Q^T ----
     f32x4 s[4][2];
@@ -157,7 +190,9 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
       }
     }
 
-    // ---- masked online softmax, one row per lane column ----
+    // ---- online softmax, one row per lane column; the mask only where the tile reaches past the first query's
+    // position (causal) or past the keys ----
+    const bool masked = kv0 + kBK > nk || (p.causal && kv0 + kBK - 1 > first_pos);
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       float tmax = -INFINITY;
@@ -166,7 +201,7 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int jj = kv0 + kt * 16 + jq * 4 + rr;
-          const bool ok = jj < nk && (!p.causal || jj <= qpos[rt]);
+          const bool ok = !masked || (jj < nk && (!p.causal || jj <= qpos[rt]));
           const float x = ok ? s[kt][rt][rr] * p.scale_log2 : -INFINITY;
           s[kt][rt][rr] = x;
           tmax = fmaxf(tmax, x);
@@ -190,7 +225,8 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
       for (int dt = 0; dt < 8; ++dt) acc[dt][rt] *= alpha;
     }
 
-    // ---- O^T[d][row] += V^T P^T; k-step ks covers keys ks*32 + [0, 32) ----
+    // ---- O^T[d][row] += V^T P^T; k-step k2 covers keys k2*32 + {jq*4 + [0,4), 16 + jq*4 + [0,4)} for lane jq, the
+    // order in which the score MFMA left P^T in the lane's registers ----
     u32x4 pb[2][2];
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2)
@@ -204,10 +240,12 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
       for (int k2 = 0; k2 < 2; ++k2) {
-        const uint16_t* row = &vts[dt * 16 + r16][k2 * 32];
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(row + jq * 4);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(row + 16 + jq * 4);
-        const u32x4 a = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        const uint16_t* vb = &vs[k2 * 32][dt * 16] + tr_off;
+        const s16x4 lo = lds_read_tr16(vb);
+        const s16x4 hi = lds_read_tr16(vb + 16 * kKsStride);
+        const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
+        const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
+        const u32x4 a = u32x4{l2[0], l2[1], h2[0], h2[1]};
         acc[dt][0] = mfma_16x16x32(a, pb[k2][0], acc[dt][0]);
         acc[dt][1] = mfma_16x16x32(a, pb[k2][1], acc[dt][1]);
       }

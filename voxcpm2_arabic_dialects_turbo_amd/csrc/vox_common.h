@@ -65,4 +65,14 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Transposed LDS read (ds_read_b64_tr_b16): within each 16-lane group, lane j returns element j%4 of the 8-byte
+// chunks that lanes 4r + j/4 (r = 0..3) address, i.e. four rows of one column when lanes 4r + q point at row r,
+// column 4q. Turns a row-major [row][col] bf16 tile into MFMA A-operand columns.
+__device__ __forceinline__ s16x4 lds_read_tr16(const uint16_t* p) {
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+}
+
 }  // namespace vox
