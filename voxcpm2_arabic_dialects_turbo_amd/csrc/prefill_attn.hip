@@ -116,6 +116,7 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
   u32x4 kr[4], vr[4];
   int bids[4] = {0, 0, 0, 0};
   unsigned live = 0;  // bit i: piece i is a real key
+  bool full = false;  // packed keys, every key of the tile real: staged without the zero selects
   auto fetch_bids = [&](int kv0) {
     if (!p.block_tables) return;
 #pragma unroll
@@ -126,6 +127,7 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
   };
   auto load_tile = [&](int kv0) {
     live = 0;
+    full = !p.block_tables && kv0 + kBK <= nk;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int pc = tid + i * 256;
@@ -151,12 +153,21 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
     }
   };
   auto stage_tile = [&]() {
+    if (full) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int pc = tid + i * 256;
-      const bool ok = (live >> i) & 1u;
-      *reinterpret_cast<u32x4*>(&ks[pc >> 4][(pc & 15) * 8]) = ok ? kr[i] : zero4();
-      *reinterpret_cast<u32x4*>(&vs[pc >> 4][(pc & 15) * 8]) = ok ? vr[i] : zero4();
+      for (int i = 0; i < 4; ++i) {
+        const int pc = tid + i * 256;
+        *reinterpret_cast<u32x4*>(&ks[pc >> 4][(pc & 15) * 8]) = kr[i];
+        *reinterpret_cast<u32x4*>(&vs[pc >> 4][(pc & 15) * 8]) = vr[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int pc = tid + i * 256;
+        const bool ok = (live >> i) & 1u;
+        *reinterpret_cast<u32x4*>(&ks[pc >> 4][(pc & 15) * 8]) = ok ? kr[i] : zero4();
+        *reinterpret_cast<u32x4*>(&vs[pc >> 4][(pc & 15) * 8]) = ok ? vr[i] : zero4();
+      }
     }
   };
   // this lane's transposed-read address inside a 16-key x 16-d block: row jq*4 + r16/4, column 4*(r16%4)
@@ -191,38 +202,54 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
     }
 
     // ---- online softmax, one row per lane column; the mask only where the tile reaches past the first query's
-    // position (causal) or past the keys ----
+    // position (causal) or past the keys. The scale goes into the exp2 argument (one FMA), and the running max moves
+    // (rescaling o and l) only when a row's tile max exceeds it by more than 8: p stays <= 256, exact after the final
+    // 1 / l, and most tiles skip the rescale ----
     const bool masked = kv0 + kBK > nk || (p.causal && kv0 + kBK - 1 > first_pos);
+    const float c = p.scale_log2;
+    float tm[2];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
-      float tmax = -INFINITY;
+      float t = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-          const int jj = kv0 + kt * 16 + jq * 4 + rr;
-          const bool ok = !masked || (jj < nk && (!p.causal || jj <= qpos[rt]));
-          const float x = ok ? s[kt][rt][rr] * p.scale_log2 : -INFINITY;
-          s[kt][rt][rr] = x;
-          tmax = fmaxf(tmax, x);
+          if (masked) {
+            const int jj = kv0 + kt * 16 + jq * 4 + rr;
+            const bool ok = jj < nk && (!p.causal || jj <= qpos[rt]);
+            s[kt][rt][rr] = ok ? s[kt][rt][rr] : -INFINITY;
+          }
+          t = fmaxf(t, s[kt][rt][rr]);
         }
-      tmax = col_max4(tmax);
-      const float m_new = fmaxf(m[rt], tmax);
-      const float mu = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = fast_exp2(m[rt] - mu);
+      tm[rt] = col_max4(t) * c;  // scaled (log2) units; c > 0
+    }
+    const bool up0 = tm[0] > m[0] + 8.f;
+    const bool up1 = tm[1] > m[1] + 8.f;
+    if (__builtin_amdgcn_ballot_w64(up0 || up1) != 0) {  // wave-uniform
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const bool up = rt == 0 ? up0 : up1;
+        const float alpha = up ? fast_exp2(m[rt] - tm[rt]) : 1.f;  // exp2(-inf) = 0 on a row's first update
+        m[rt] = up ? tm[rt] : m[rt];
+        l[rt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) acc[dt][rt] *= alpha;
+      }
+    }
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const float mu = m[rt] == -INFINITY ? 0.f : m[rt];
       float ps = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-          const float e = fast_exp2(s[kt][rt][rr] - mu);
+          const float e = fast_exp2(fmaf(s[kt][rt][rr], c, -mu));
           s[kt][rt][rr] = e;
           ps += e;
         }
-      l[rt] = l[rt] * alpha + ps;
-      m[rt] = m_new;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) acc[dt][rt] *= alpha;
+      l[rt] += ps;
     }
 
     // ---- O^T[d][row] += V^T P^T; k-step k2 covers keys k2*32 + {jq*4 + [0,4), 16 + jq*4 + [0,4)} for lane jq, the
