@@ -192,6 +192,12 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
       for (int kq = 0; kq < 4; ++kq) qv[kq] = ld_g16(qb + kq * 32);
     }
 
+    // the score MFMA's B operands for the segment: block-diagonal over (kv head, d)
+    u32x4 qop[TT::KC];
+#pragma unroll
+    for (int kc = 0; kc < TT::KC; ++kc) qop[kc] = hg == kc / 4 ? qv[kc % 4] : zero4();
+    const float c = p.scale_log2;
+
     float m = -INFINITY;
     float lsum = 0.f;
     f32x4 acc[8];
@@ -203,42 +209,52 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
       T.ok = blk >= 0 && blk < p.num_blocks;
       load_tile<HK>(T, p, (T.ok ? blk : 0) * p.block_size + (t0 % p.block_size), r16, jq, lane);
     };
-    // Scores, online softmax and P V of one loaded tile.
+    // Scores, online softmax and P V of one loaded tile. The scale goes into the exp2 argument (one FMA); the running
+    // max moves (rescaling acc and lsum) only when the tile max exceeds it by more than 8 in log2 units (p <= 256,
+    // exact after the final 1 / l); the masks and zero selects run only on a tile that is not fully valid.
     auto compute = [&](const Tile<HK>& T, int t0) {
       f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kc = 0; kc < TT::KC; ++kc) s = mfma_16x16x32(T.k[kc], hg == kc / 4 ? qv[kc % 4] : zero4(), s);
+      for (int kc = 0; kc < TT::KC; ++kc) s = mfma_16x16x32(T.k[kc], qop[kc], s);
+      const bool full = T.ok && t0 + kTile <= tok_end;  // wave-uniform
       // lane (head r16) holds tokens t0 + jq*4 + [0, 4)
       float x[4];
-      float tmax = -INFINITY;
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const bool ok = T.ok && (t0 + jq * 4 + rr) < tok_end;
-        x[rr] = ok ? s[rr] * p.scale_log2 : -INFINITY;
-        tmax = fmaxf(tmax, x[rr]);
+      for (int rr = 0; rr < 4; ++rr)
+        x[rr] = full || (T.ok && (t0 + jq * 4 + rr) < tok_end) ? s[rr] : -INFINITY;
+      const float tm = col_max4(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]))) * c;
+      const bool up = tm > m + 8.f;
+      if (__builtin_amdgcn_ballot_w64(up) != 0) {  // wave-uniform
+        const float alpha = up ? fast_exp2(m - tm) : 1.f;  // exp2(-inf) = 0 on the first update
+        m = up ? tm : m;
+        lsum *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
       }
-      tmax = col_max4(tmax);
-      const float m_new = fmaxf(m, tmax);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = fast_exp2(m - m_use);
+      const float mu = m == -INFINITY ? 0.f : m;
       float ps = 0.f;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        x[rr] = fast_exp2(x[rr] - m_use);
+        x[rr] = fast_exp2(fmaf(x[rr], c, -mu));
         ps += x[rr];
       }
-      lsum = lsum * alpha + ps;
-      m = m_new;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+      lsum += ps;
 
       // V tile -> LDS, row-major, 16-byte stores; rows of tokens past tok_end or of an unmapped block are zeroed
       // (they meet p = 0 in P V, and unwritten cache slots may hold any bit pattern)
+      if (full) {
 #pragma unroll
-      for (int i = 0; i < TT::VP; ++i) {
-        const int pc = i * 64 + lane;
-        const bool ok = T.ok && (t0 + pc / TT::PPR) < tok_end;
-        *reinterpret_cast<u32x4*>(vt + (pc / TT::PPR) * VROW + (pc % TT::PPR) * 8) = ok ? T.v[i] : zero4();
+        for (int i = 0; i < TT::VP; ++i) {
+          const int pc = i * 64 + lane;
+          *reinterpret_cast<u32x4*>(vt + (pc / TT::PPR) * VROW + (pc % TT::PPR) * 8) = T.v[i];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < TT::VP; ++i) {
+          const int pc = i * 64 + lane;
+          const bool ok = T.ok && (t0 + pc / TT::PPR) < tok_end;
+          *reinterpret_cast<u32x4*>(vt + (pc / TT::PPR) * VROW + (pc % TT::PPR) * 8) = ok ? T.v[i] : zero4();
+        }
       }
       wave_lds_sync();
 
