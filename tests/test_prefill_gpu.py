@@ -153,6 +153,21 @@ def test_zero_length_sequences_in_a_padded_batch():
     attn_close(out, want, "zero-length sequences")
 
 
+@pytest.mark.parametrize("bs", [32, 64, 128, 512])
+def test_paged_block_sizes(bs):
+    """Both paged key paths: a block size that is a multiple of the 64-key tile (one block id per tile) and one
+    that is not (32: one block id per 16-byte piece), over cached prefixes with ragged last tiles."""
+    gen = torch.Generator().manual_seed(56 + bs)
+    nq = [37, 1, 130, 64]
+    nk = [37 + 90, 1 + 700, 130, 64 + 63]
+    kc, vc, tables = paged_pool(gen, nk, sum((n + bs - 1) // bs for n in nk) + 3, block_size=bs)
+    q = randn(gen, sum(nq), H, D)
+    out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), max(nq), _cu(nq).to(DEV), max(nk),
+                                 _cu(nk).to(DEV), softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
+    want = ref.varlen(q.float(), _cu(nq), _cu(nk), k_cache=kc, v_cache=vc, block_tables=tables)
+    attn_close(out, want, f"paged block_size {bs}")
+
+
 @pytest.mark.parametrize("h,hk", [(16, 1), (8, 1), (16, 4), (4, 4)])
 def test_group_sizes(h, hk):
     gen = torch.Generator().manual_seed(54 + h + hk)

@@ -188,6 +188,8 @@ int prefill_setup(const char* fn, const void* q, int64_t q_row_stride, const voi
     if (key_row_stride < (int64_t)num_kv_heads * head_dim || value_row_stride < (int64_t)num_kv_heads * head_dim ||
         key_row_stride % 8 || value_row_stride % 8 || !aligned16(key) || !aligned16(value))
       return fail(VOX_EINVAL, "%s: key/value must be 16-byte aligned rows, stride multiple of 8", fn);
+    if (key_row_stride >= (1 << 24) || value_row_stride >= (1 << 24))
+      return fail(VOX_EINVAL, "%s: key/value row stride must be below 2^24 elements", fn);
   }
   *a = vox::PrefillArgs{};
   a->q = (const uint16_t*)q;

@@ -36,7 +36,12 @@ constexpr int kRows = 128;       // query rows per workgroup
 constexpr int kKsStride = kD + 8;   // LDS K / V row: 128 d + 8 pad (bf16); 16 consecutive rows of a transposed
                                     // read then cover every bank exactly twice
 
-template <bool QUANT>
+// Where a workgroup's keys come from (one kernel instance each, so no path's loop-carried state constrains another's
+// load waits): packed [Tk, HK, D] rows; the paged cache with block_size a multiple of 64 (a 64-key tile lies in one
+// block: one block id per tile); the paged cache with any other block size (one block id per 16-byte piece).
+enum KvSource { kPacked = 0, kPagedTiles = 1, kPagedPieces = 2 };
+
+template <bool QUANT, int KV>
 __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kernel(PrefillArgs p) {
   constexpr int NH = QUANT ? 2 : 1;  // KV-group halves per workgroup
   __shared__ __attribute__((aligned(16))) uint16_t ks_all[NH][kBK][kKsStride];
@@ -64,7 +69,7 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
     k0 = b * p.uniform_k;
     nk = p.uniform_k;
   }
-  if (p.block_tables) nk = min(nk, p.max_blocks * p.block_size);  // keys the block table can address
+  if (KV != kPacked) nk = min(nk, p.max_blocks * p.block_size);  // keys the block table can address
   const int G = p.group;
   const int BQ = kRows / G;  // query tokens per workgroup
   if (qt * BQ >= nq) return;
@@ -97,6 +102,7 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) qop[rt][kc] = row_ok[rt] ? ld_g16(qp + kc * 32) : zero4();
   }
+  wait_vmem_all();
 
   const int tq_last = min(nq, (qt + 1) * BQ) - 1;
   const int kv_end = p.causal ? min(nk, nk - nq + tq_last + 1) : nk;
@@ -109,47 +115,73 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) acc[dt][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // ---- K/V tile loads: 4 + 4 pieces of 16 bytes per thread (key kk = pc / 16, dims dc .. dc + 8), unconditional
-  // and in bounds (a key past nk or in an unmapped block reads a valid address and is zeroed when staged). In paged
-  // mode the pieces' block ids are read one tile ahead (fetch_bids), so a tile's eight loads issue back to back
-  // instead of each waiting on its own lookup.
+  // ---- K/V tile loads: 4 + 4 pieces of 16 bytes per thread (piece i: key lrow + 16 i of the tile, dims dc .. dc + 8),
+  // unconditional and in bounds (a key past nk reads the tile's last real key or, in a paged tile, a slot of the same
+  // block; an unmapped block reads block 0; either is zeroed when staged). Packed keys and paged tiles that lie inside
+  // one cache block (block_size a multiple of 64) address a tile from one uniform base plus a 32-bit lane offset, with
+  // the tile's block id read one tile ahead; other block sizes read each piece's block id one tile ahead
+  // (fetch_bids), so a tile's eight loads still issue back to back.
+  constexpr bool paged = KV != kPacked;
+  constexpr bool blk_tiles = KV == kPagedTiles;
+  const int rs_k = paged ? HK * kD : (int)p.k_row_stride;  // elements between consecutive keys (< 2^24)
+  const int rs_v = paged ? HK * kD : (int)p.v_row_stride;
+  const int lrow = tid >> 4;
+  const int dc = (tid & 15) * 8;
   u32x4 kr[4], vr[4];
-  int bids[4] = {0, 0, 0, 0};
-  unsigned live = 0;  // bit i: piece i is a real key
-  bool full = false;  // packed keys, every key of the tile real: staged without the zero selects
+  int bids[4] = {0, 0, 0, 0};  // per-piece block ids (paged, block_size not a multiple of 64)
+  int tile_bid = 0;            // the block id of the next tile to load (paged, block_size a multiple of 64)
+  unsigned live = 0;           // bit i: piece i is a real key
+  bool full = false;           // every key of the tile real: staged without the zero selects
   auto fetch_bids = [&](int kv0) {
-    if (!p.block_tables) return;
+    if constexpr (!paged) return;
+    if constexpr (blk_tiles) {
+      tile_bid = p.block_tables[(int64_t)b * p.bt_stride + min(kv0, nk - 1) / p.block_size];
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int jc = min(kv0 + (tid >> 4) + 16 * i, nk - 1);
+      const int jc = min(kv0 + lrow + 16 * i, nk - 1);
       bids[i] = p.block_tables[(int64_t)b * p.bt_stride + jc / p.block_size];
     }
   };
   auto load_tile = [&](int kv0) {
+    const int lim = min(kBK, nk - kv0) - 1;  // the tile's last real key, relative (>= 0)
+    if constexpr (!paged || blk_tiles) {
+      const uint16_t* kb;
+      const uint16_t* vb;
+      bool okb = true;
+      if constexpr (!paged) {
+        kb = p.k_src + (int64_t)(k0 + kv0) * p.k_row_stride + g * kD;
+        vb = p.v_src + (int64_t)(k0 + kv0) * p.v_row_stride + g * kD;
+      } else {
+        okb = tile_bid >= 0 && tile_bid < p.num_blocks;
+        const int64_t row0 = (int64_t)(okb ? tile_bid : 0) * p.block_size + kv0 % p.block_size;
+        kb = p.k_cache + row0 * rs_k + g * kD;
+        vb = p.v_cache + row0 * rs_k + g * kD;
+      }
+      full = okb && lim == kBK - 1;
+      live = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = min(lrow + 16 * i, lim);
+        kr[i] = ld_g16(kb + (uint32_t)(r * rs_k + dc));
+        vr[i] = ld_g16(vb + (uint32_t)(r * rs_v + dc));
+        live |= (okb && lrow + 16 * i <= lim ? 1u : 0u) << i;
+      }
+    } else {
     live = 0;
-    full = !p.block_tables && kv0 + kBK <= nk;
+    full = false;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int pc = tid + i * 256;
-      const int dc = (pc & 15) * 8;
-      const int jj = kv0 + (pc >> 4);
+      const int jj = kv0 + lrow + 16 * i;
       const int jc = min(jj, nk - 1);
-      const uint16_t* kp;
-      const uint16_t* vp;
-      bool ok = jj < nk;
-      if (p.block_tables) {
-        const int64_t blk = bids[i];
-        ok = ok && blk >= 0 && blk < p.num_blocks;
-        const int64_t off = (((ok ? blk : 0) * p.block_size + jc % p.block_size) * HK + g) * kD + dc;
-        kp = p.k_cache + off;
-        vp = p.v_cache + off;
-      } else {
-        kp = p.k_src + (int64_t)(k0 + jc) * p.k_row_stride + g * kD + dc;
-        vp = p.v_src + (int64_t)(k0 + jc) * p.v_row_stride + g * kD + dc;
-      }
-      kr[i] = ld_g16(kp);
-      vr[i] = ld_g16(vp);
+      const int64_t blk = bids[i];
+      const bool ok = jj < nk && blk >= 0 && blk < p.num_blocks;
+      const int64_t off = (((ok ? blk : 0) * p.block_size + jc % p.block_size) * HK + g) * kD + dc;
+      kr[i] = ld_g16(p.k_cache + off);
+      vr[i] = ld_g16(p.v_cache + off);
       live |= (ok ? 1u : 0u) << i;
+    }
     }
   };
   auto stage_tile = [&]() {
@@ -338,13 +370,23 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
 
 }  // namespace
 
+template <bool QUANT>
+hipError_t launch_prefill_kind(const PrefillArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
+  if (!a.block_tables)
+    prefill_kernel<QUANT, kPacked><<<grid, block, 0, stream>>>(a);
+  else if (a.block_size % kBK == 0)
+    prefill_kernel<QUANT, kPagedTiles><<<grid, block, 0, stream>>>(a);
+  else
+    prefill_kernel<QUANT, kPagedPieces><<<grid, block, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
 hipError_t launch_prefill(const PrefillArgs& a, int max_seqlen_q, hipStream_t stream) {
   const int bq = kRows / a.group;
   const int q_tiles = (max_seqlen_q + bq - 1) / bq;
   if (q_tiles <= 0 || a.batch <= 0) return hipSuccess;
-  dim3 grid((unsigned)q_tiles, (unsigned)a.batch, (unsigned)a.num_kv_heads);
-  prefill_kernel<false><<<grid, dim3(256), 0, stream>>>(a);
-  return hipGetLastError();
+  return launch_prefill_kind<false>(a, dim3((unsigned)q_tiles, (unsigned)a.batch, (unsigned)a.num_kv_heads), dim3(256),
+                                    stream);
 }
 
 hipError_t launch_prefill_int8(const PrefillArgs& a, int max_seqlen_q, hipStream_t stream) {
@@ -352,9 +394,8 @@ hipError_t launch_prefill_int8(const PrefillArgs& a, int max_seqlen_q, hipStream
   const int q_tiles = (max_seqlen_q + bq - 1) / bq;
   if (q_tiles <= 0 || a.batch <= 0) return hipSuccess;
   if (a.num_kv_heads < 1 || a.num_kv_heads > 2) return hipErrorInvalidValue;
-  dim3 grid((unsigned)q_tiles, (unsigned)a.batch, 1u);
-  prefill_kernel<true><<<grid, dim3(256 * a.num_kv_heads), 0, stream>>>(a);
-  return hipGetLastError();
+  return launch_prefill_kind<true>(a, dim3((unsigned)q_tiles, (unsigned)a.batch, 1u), dim3(256 * a.num_kv_heads),
+                                   stream);
 }
 
 }  // namespace vox

@@ -34,10 +34,9 @@ __device__ __forceinline__ u32x4 ld_g16(const void* p) { return *reinterpret_cas
 
 // Round-to-nearest-even fp32 -> bf16 of two values packed low/high into one dword.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  __bf16 a = static_cast<__bf16>(lo);
-  __bf16 b = static_cast<__bf16>(hi);
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), bf16x2));  // one v_cvt_pk_bf16_f32
 }
 
 __device__ __forceinline__ float bf16_bits_to_float(uint32_t bits16) {
@@ -45,18 +44,38 @@ __device__ __forceinline__ float bf16_bits_to_float(uint32_t bits16) {
 }
 
 // Max / sum over the four lanes {l, l^16, l^32, l^48} that share l%16 (one MFMA column).
-__device__ __forceinline__ float col_max4(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16, kWave));
-  x = fmaxf(x, __shfl_xor(x, 32, kWave));
-  return x;
+// Cross-row exchanges of a wavefront without LDS: v_permlane32_swap exchanges the two 32-lane halves between its
+// operands, v_permlane16_swap the odd 16-lane rows of one with the even rows of the other. Called with the same
+// value twice, the two results hold (in some order) x of each lane and x of its partner 32 (16) lanes away, so the
+// max or sum of the pair is the same in both partners whichever operand the hardware swaps.
+__device__ __forceinline__ float xhalf_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
-__device__ __forceinline__ float col_sum4(float x) {
-  x += __shfl_xor(x, 16, kWave);
-  x += __shfl_xor(x, 32, kWave);
-  return x;
+__device__ __forceinline__ float xrow_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xhalf_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xrow_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Max / sum over the four lanes l % 16 + 16 j (j = 0..3): an MFMA D column spread over the four 16-lane rows.
+__device__ __forceinline__ float col_max4(float x) { return xrow_max(xhalf_max(x)); }
+__device__ __forceinline__ float col_sum4(float x) { return xrow_sum(xhalf_sum(x)); }
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// s_waitcnt vmcnt(0): every vector memory load of this wave has landed. Placed after loads whose registers stay live
+// across a software-pipelined loop (the query operands), it lets the compiler's wait analysis see them as complete
+// at the loop header; otherwise it falls back to a full vmcnt(0) inside the loop, which also waits for the
+// next tile's prefetch.
+__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Orders this wavefront's LDS writes before its later LDS reads of other lanes' data (wave-private buffers).
 __device__ __forceinline__ void wave_lds_sync() {
