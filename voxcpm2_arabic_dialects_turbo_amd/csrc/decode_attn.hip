@@ -58,19 +58,19 @@ struct Tile {
 // Issues the loads of the 16-token tile whose first token sits at cache slot slot0 (a tile never straddles a cache
 // block). Every load is unconditional and in bounds, so the compiler can count outstanding loads exactly: the caller
 // maps an unmapped block to block 0 and masks what it read. K rows land in MFMA A layout (lane = token r16), V
-// pieces coalesced (16 bytes per lane, whole slot rows per instruction).
+// pieces coalesced (16 bytes per lane, whole slot rows per instruction). slot0 is wave-uniform: each load is a
+// uniform base plus a per-lane 32-bit byte offset that is the same for every tile (koff, voff) plus an immediate.
 template <int HK>
-__device__ __forceinline__ void load_tile(Tile<HK>& T, const DecodeArgs& p, int64_t slot0, int r16, int jq,
-                                          int lane) {
+__device__ __forceinline__ void load_tile(Tile<HK>& T, const DecodeArgs& p, int64_t slot0, uint32_t koff,
+                                          uint32_t voff) {
   using TT = Tile<HK>;
-  const uint16_t* kp = p.k_cache + (slot0 + r16) * TT::ROW + jq * 8;
+  const char* kb = reinterpret_cast<const char*>(p.k_cache + slot0 * TT::ROW) + koff;
+  const char* vb = reinterpret_cast<const char*>(p.v_cache + slot0 * TT::ROW) + voff;
 #pragma unroll
-  for (int kc = 0; kc < TT::KC; ++kc) T.k[kc] = ld_g16(kp + kc * 32);
+  for (int kc = 0; kc < TT::KC; ++kc) T.k[kc] = ld_g16(kb + kc * 64);
+  // V piece i covers 64 / PPR slot rows starting at row i * 64 / PPR: i * 1024 bytes past piece 0 for any HK
 #pragma unroll
-  for (int i = 0; i < TT::VP; ++i) {
-    const int pc = i * 64 + lane;
-    T.v[i] = ld_g16(p.v_cache + (slot0 + pc / TT::PPR) * TT::ROW + (pc % TT::PPR) * 8);
-  }
+  for (int i = 0; i < TT::VP; ++i) T.v[i] = ld_g16(vb + i * 1024);
 }
 
 // A value every lane of the wave holds, moved to a scalar register (LDS reads land in vector registers).
@@ -191,6 +191,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
 #pragma unroll
       for (int kq = 0; kq < 4; ++kq) qv[kq] = ld_g16(qb + kq * 32);
     }
+    wait_vmem_all();  // the query is complete before the tile loop, whose waits then count tile loads only
 
     // the score MFMA's B operands for the segment: block-diagonal over (kv head, d)
     u32x4 qop[TT::KC];
@@ -204,10 +205,14 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    // per-lane byte offsets of the tile loads: K row r16, dims jq*8 + [0, 8) (+ 32 per k-step); V piece 0 = row
+    // lane / PPR, dims (lane % PPR) * 8 + [0, 8)
+    const uint32_t koff = (uint32_t)(r16 * TT::ROW + jq * 8) * 2u;
+    const uint32_t voff = (uint32_t)((lane / TT::PPR) * TT::ROW + (lane % TT::PPR) * 8) * 2u;
     // Issues the loads of the tile at token t0 of cache block blk.
     auto issue = [&](Tile<HK>& T, int64_t blk, int t0) {
       T.ok = blk >= 0 && blk < p.num_blocks;
-      load_tile<HK>(T, p, (T.ok ? blk : 0) * p.block_size + (t0 % p.block_size), r16, jq, lane);
+      load_tile<HK>(T, p, (T.ok ? blk : 0) * p.block_size + (t0 % p.block_size), koff, voff);
     };
     // Scores, online softmax and P V of one loaded tile. The scale goes into the exp2 argument (one FMA); the running
     // max moves (rescaling acc and lsum) only when the tile max exceeds it by more than 8 in log2 units (p <= 256,

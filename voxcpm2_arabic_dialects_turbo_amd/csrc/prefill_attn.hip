@@ -45,7 +45,7 @@ template <bool QUANT, int KV>
 __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kernel(PrefillArgs p) {
   constexpr int NH = QUANT ? 2 : 1;  // KV-group halves per workgroup
   __shared__ __attribute__((aligned(16))) uint16_t ks_all[NH][kBK][kKsStride];
-  __shared__ __attribute__((aligned(16))) uint16_t vs_all[NH][kBK][kKsStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vs_all[NH][2][kBK][kKsStride];  // V double-buffered
   __shared__ unsigned s_amax[QUANT ? kRows : 1];  // QUANT: per token of the tile, float bits of max |o|
 
   const int qt = blockIdx.x;
@@ -53,7 +53,7 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
   const int half = QUANT ? (int)(threadIdx.x >> 8) : 0;
   const int g = QUANT ? half : (int)blockIdx.z;
   auto& ks = ks_all[half];
-  auto& vs = vs_all[half];
+  auto& vs2 = vs_all[half];
   int q0, nq, k0, nk;
   if (p.cu_q) {
     q0 = p.cu_q[b];
@@ -184,7 +184,8 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
     }
     }
   };
-  auto stage_tile = [&]() {
+  auto stage_tile = [&](int vb) {
+    auto& vs = vs2[vb];
     if (full) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -211,104 +212,144 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
     load_tile(0);
     fetch_bids(kBK);
   }
-  for (int kv0 = 0; kv0 < kv_end; kv0 += kBK) {
-    stage_tile();
-    __syncthreads();
-    if (kv0 + kBK < kv_end) {  // in flight while this tile computes
-      load_tile(kv0 + kBK);
-      fetch_bids(kv0 + 2 * kBK);
-    }
-
-    // ---- S^T[key][row] = K Q^T ----
-    f32x4 s[4][2];
+  // ---- per-tile steps. The loop is software-pipelined: P V of tile j - 1 (V from the other LDS buffer, P from
+  // registers) runs in the same instruction block as tile j's softmax, so its MFMAs and transposed reads interleave
+  // with the softmax VALU work; K is single-buffered (only tile j's scores read it).
+  auto scores = [&](f32x4 (&sc)[4][2]) {  // S^T[key][row] = K Q^T
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
-      s[kt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-      s[kt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      sc[kt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+      sc[kt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
         const u32x4 a = *reinterpret_cast<const u32x4*>(&ks[kt * 16 + r16][kc * 32 + jq * 8]);
-        s[kt][0] = mfma_16x16x32(a, qop[0][kc], s[kt][0]);
-        s[kt][1] = mfma_16x16x32(a, qop[1][kc], s[kt][1]);
+        sc[kt][0] = mfma_16x16x32(a, qop[0][kc], sc[kt][0]);
+        sc[kt][1] = mfma_16x16x32(a, qop[1][kc], sc[kt][1]);
       }
     }
-
-    // ---- online softmax, one row per lane column; the mask only where the tile reaches past the first query's
-    // position (causal) or past the keys. The scale goes into the exp2 argument (one FMA), and the running max moves
-    // (rescaling o and l) only when a row's tile max exceeds it by more than 8: p stays <= 256, exact after the final
-    // 1 / l, and most tiles skip the rescale ----
-    const bool masked = kv0 + kBK > nk || (p.causal && kv0 + kBK - 1 > first_pos);
+  };
+  // The causal / length mask, only where the tile reaches past the first query's position or past the keys.
+  auto mask = [&](f32x4 (&sc)[4][2], int kv0) {
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int jj = kv0 + kt * 16 + jq * 4 + rr;
+          const bool ok = jj < nk && (!p.causal || jj <= qpos[rt]);
+          sc[kt][rt][rr] = ok ? sc[kt][rt][rr] : -INFINITY;
+        }
+  };
+  // Online softmax, one row per lane column, branch-free. The scale goes into the exp2 argument (one FMA); a row's
+  // running max moves only when its tile max exceeds it by more than 8 in log2 units (p <= 256, exact after the
+  // final 1 / l), so most tiles leave the accumulators alone. Returns whether any row of the wave moved; alpha is
+  // the factor (1 for rows that did not move) that the accumulators, which still hold the previous tile's P V at
+  // the old max, need once that P V has been added.
+  auto softmax = [&](f32x4 (&sc)[4][2], u32x4 (&pbo)[2][2], float (&alpha)[2]) -> bool {
     const float c = p.scale_log2;
-    float tm[2];
+    bool up[2];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       float t = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          if (masked) {
-            const int jj = kv0 + kt * 16 + jq * 4 + rr;
-            const bool ok = jj < nk && (!p.causal || jj <= qpos[rt]);
-            s[kt][rt][rr] = ok ? s[kt][rt][rr] : -INFINITY;
-          }
-          t = fmaxf(t, s[kt][rt][rr]);
-        }
-      tm[rt] = col_max4(t) * c;  // scaled (log2) units; c > 0
-    }
-    const bool up0 = tm[0] > m[0] + 8.f;
-    const bool up1 = tm[1] > m[1] + 8.f;
-    if (__builtin_amdgcn_ballot_w64(up0 || up1) != 0) {  // wave-uniform
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        const bool up = rt == 0 ? up0 : up1;
-        const float alpha = up ? fast_exp2(m[rt] - tm[rt]) : 1.f;  // exp2(-inf) = 0 on a row's first update
-        m[rt] = up ? tm[rt] : m[rt];
-        l[rt] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) acc[dt][rt] *= alpha;
-      }
-    }
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+        t = fmaxf(t, fmaxf(fmaxf(sc[kt][rt][0], sc[kt][rt][1]), fmaxf(sc[kt][rt][2], sc[kt][rt][3])));
+      const float tm = col_max4(t) * c;  // scaled (log2) units; c > 0
+      up[rt] = tm > m[rt] + 8.f;
+      alpha[rt] = up[rt] ? fast_exp2(m[rt] - tm) : 1.f;  // exp2(-inf) = 0 on a row's first update
+      m[rt] = up[rt] ? tm : m[rt];
       const float mu = m[rt] == -INFINITY ? 0.f : m[rt];
       float ps = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-          const float e = fast_exp2(fmaf(s[kt][rt][rr], c, -mu));
-          s[kt][rt][rr] = e;
+          const float e = fast_exp2(fmaf(sc[kt][rt][rr], c, -mu));
+          sc[kt][rt][rr] = e;
           ps += e;
         }
-      l[rt] += ps;
+      l[rt] = l[rt] * alpha[rt] + ps;
     }
-
-    // ---- O^T[d][row] += V^T P^T; k-step k2 covers keys k2*32 + {jq*4 + [0,4), 16 + jq*4 + [0,4)} for lane jq, the
-    // order in which the score MFMA left P^T in the lane's registers ----
-    u32x4 pb[2][2];
+    // P^T B operands; k-step k2 covers keys k2*32 + {jq*4 + [0,4), 16 + jq*4 + [0,4)} for lane jq, the order in
+    // which the score MFMA left them in the lane's registers
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt)
-        pb[k2][rt] = u32x4{pack_bf16x2(s[2 * k2][rt][0], s[2 * k2][rt][1]),
-                           pack_bf16x2(s[2 * k2][rt][2], s[2 * k2][rt][3]),
-                           pack_bf16x2(s[2 * k2 + 1][rt][0], s[2 * k2 + 1][rt][1]),
-                           pack_bf16x2(s[2 * k2 + 1][rt][2], s[2 * k2 + 1][rt][3])};
+        pbo[k2][rt] = u32x4{pack_bf16x2(sc[2 * k2][rt][0], sc[2 * k2][rt][1]),
+                            pack_bf16x2(sc[2 * k2][rt][2], sc[2 * k2][rt][3]),
+                            pack_bf16x2(sc[2 * k2 + 1][rt][0], sc[2 * k2 + 1][rt][1]),
+                            pack_bf16x2(sc[2 * k2 + 1][rt][2], sc[2 * k2 + 1][rt][3])};
+    return __builtin_amdgcn_ballot_w64(up[0] || up[1]) != 0;
+  };
+  // O^T[d][row] += V^T P^T over one tile; V^T from the LDS buffer vb with two transposed reads per 8-key column
+  auto pv = [&](const u32x4 (&pbi)[2][2], int vb) {
+    auto& vs = vs2[vb];
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
       for (int k2 = 0; k2 < 2; ++k2) {
-        const uint16_t* vb = &vs[k2 * 32][dt * 16] + tr_off;
-        const s16x4 lo = lds_read_tr16(vb);
-        const s16x4 hi = lds_read_tr16(vb + 16 * kKsStride);
+        const uint16_t* vp = &vs[k2 * 32][dt * 16] + tr_off;
+        const s16x4 lo = lds_read_tr16(vp);
+        const s16x4 hi = lds_read_tr16(vp + 16 * kKsStride);
         const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
         const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
         const u32x4 a = u32x4{l2[0], l2[1], h2[0], h2[1]};
-        acc[dt][0] = mfma_16x16x32(a, pb[k2][0], acc[dt][0]);
-        acc[dt][1] = mfma_16x16x32(a, pb[k2][1], acc[dt][1]);
+        acc[dt][0] = mfma_16x16x32(a, pbi[k2][0], acc[dt][0]);
+        acc[dt][1] = mfma_16x16x32(a, pbi[k2][1], acc[dt][1]);
       }
+  };
+
+  // The per-piece block-id path keeps eight more live registers; it runs the steps in order instead (no spills).
+  constexpr bool kPipelined = KV != kPagedPieces;
+  u32x4 pbp[2][2];  // P^T of the previous tile, waiting for its P V
+  float alpha[2] = {1.f, 1.f};  // the last softmax's accumulator factors
+  bool moved = false;           // ... and whether any of them is not 1
+  auto rescale = [&]() {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      acc[dt][0] *= alpha[0];
+      acc[dt][1] *= alpha[1];
+    }
+  };
+  int vb = 0;       // LDS buffer of this tile's V
+  for (int kv0 = 0; kv0 < kv_end; kv0 += kBK) {
+    stage_tile(vb);
     __syncthreads();
+    if (kv0 + kBK < kv_end) {  // in flight while this tile computes
+      load_tile(kv0 + kBK);
+      fetch_bids(kv0 + 2 * kBK);
+    }
+    // the previous tile's max move, now that its P V (which used the old max) is in the accumulators; done here
+    // rather than after the softmax so that no branch splits the softmax from the P V it interleaves with
+    if (kPipelined && moved) rescale();
+    f32x4 sc[4][2];
+    scores(sc);
+    if (kv0 + kBK > nk || (p.causal && kv0 + kBK - 1 > first_pos)) mask(sc, kv0);
+    u32x4 pb[2][2];
+    if constexpr (kPipelined) {
+      if (kv0 == 0) {
+        moved = softmax(sc, pb, alpha);
+      } else {
+        moved = softmax(sc, pb, alpha);
+        pv(pbp, vb ^ 1);
+      }
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2) {
+        pbp[k2][0] = pb[k2][0];
+        pbp[k2][1] = pb[k2][1];
+      }
+    } else {
+      if (softmax(sc, pb, alpha)) rescale();
+      pv(pb, vb);
+    }
+    vb ^= 1;
+    __syncthreads();  // K and the previous V buffer are free for the next tile's staging
+  }
+  if (kPipelined && kv_end > 0) {
+    if (moved) rescale();
+    pv(pbp, vb ^ 1);
   }
 
   if constexpr (QUANT) {
