@@ -33,8 +33,11 @@ namespace {
 constexpr int kD = 128;
 constexpr int kBK = 64;          // keys per tile
 constexpr int kRows = 128;       // query rows per workgroup
-constexpr int kKsStride = kD + 8;   // LDS K / V row: 128 d + 8 pad (bf16); 16 consecutive rows of a transposed
-                                    // read then cover every bank exactly twice
+// LDS row strides (bf16 elements) of the K and V tiles, chosen by measuring the kernel's own access patterns on
+// gfx950: the K-fragment 16-byte reads run 1.7x faster at 144 than at 136 (and 4-8x faster than at 128 or 132),
+// the transposed V reads are fastest from 152 up; the 16-byte staging writes do not care.
+constexpr int kKsStride = kD + 16;
+constexpr int kVsStride = kD + 24;
 
 // Where a workgroup's keys come from (one kernel instance each, so no path's loop-carried state constrains another's
 // load waits): packed [Tk, HK, D] rows; the paged cache with block_size a multiple of 64 (a 64-key tile lies in one
@@ -45,7 +48,7 @@ template <bool QUANT, int KV>
 __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kernel(PrefillArgs p) {
   constexpr int NH = QUANT ? 2 : 1;  // KV-group halves per workgroup
   __shared__ __attribute__((aligned(16))) uint16_t ks_all[NH][kBK][kKsStride];
-  __shared__ __attribute__((aligned(16))) uint16_t vs_all[NH][2][kBK][kKsStride];  // V double-buffered
+  __shared__ __attribute__((aligned(16))) uint16_t vs_all[NH][2][kBK][kVsStride];  // V double-buffered
   __shared__ unsigned s_amax[QUANT ? kRows : 1];  // QUANT: per token of the tile, float bits of max |o|
 
   const int qt = blockIdx.x;
@@ -204,7 +207,7 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
     }
   };
   // this lane's transposed-read address inside a 16-key x 16-d block: row jq*4 + r16/4, column 4*(r16%4)
-  const int tr_off = (jq * 4 + (r16 >> 2)) * kKsStride + 4 * (r16 & 3);
+  const int tr_off = (jq * 4 + (r16 >> 2)) * kVsStride + 4 * (r16 & 3);
   const int first_pos = nk - nq + qt * BQ;  // the position of the tile's first query token
 
   if (kv_end > 0) {
@@ -283,6 +286,36 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
                             pack_bf16x2(sc[2 * k2 + 1][rt][2], sc[2 * k2 + 1][rt][3])};
     return __builtin_amdgcn_ballot_w64(up[0] || up[1]) != 0;
   };
+  // Softmax against the running max as it stands (no tile max, no cross-lane step): p = exp2(s c - m). Valid
+  // while every p stays <= 2^62, which the lane's partial row sums (each at least its largest term) check;
+  // otherwise the caller redoes the tile through softmax (tile max, rescale). ps gets the lane's partial row sums.
+  // Returns whether any lane of the wave failed the check. A tile's scores rarely pass the running max by 62
+  // (log2 units) once the first tile has set it, and p of that size loses nothing in bf16 or in the fp32 sums.
+  auto softmax_fixed = [&](const f32x4 (&sc)[4][2], u32x4 (&pbo)[2][2], float (&ps)[2]) -> bool {
+    const float c = p.scale_log2;
+    bool big = false;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const float mu = m[rt] == -INFINITY ? 0.f : m[rt];
+      float sum = 0.f;
+      uint32_t pk[8];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const float e0 = fast_exp2(fmaf(sc[kt][rt][2 * h2], c, -mu));
+          const float e1 = fast_exp2(fmaf(sc[kt][rt][2 * h2 + 1], c, -mu));
+          sum += e0;
+          sum += e1;
+          pk[kt * 2 + h2] = pack_bf16x2(e0, e1);
+        }
+      ps[rt] = sum;
+      big = big || !(sum <= 0x1p62f);  // also catches inf
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2) pbo[k2][rt] = u32x4{pk[4 * k2], pk[4 * k2 + 1], pk[4 * k2 + 2], pk[4 * k2 + 3]};
+    }
+    return __builtin_amdgcn_ballot_w64(big) != 0;
+  };
   // O^T[d][row] += V^T P^T over one tile; V^T from the LDS buffer vb with two transposed reads per 8-key column
   auto pv = [&](const u32x4 (&pbi)[2][2], int vb) {
     auto& vs = vs2[vb];
@@ -292,7 +325,7 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
       for (int k2 = 0; k2 < 2; ++k2) {
         const uint16_t* vp = &vs[k2 * 32][dt * 16] + tr_off;
         const s16x4 lo = lds_read_tr16(vp);
-        const s16x4 hi = lds_read_tr16(vp + 16 * kKsStride);
+        const s16x4 hi = lds_read_tr16(vp + 16 * kVsStride);
         const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
         const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
         const u32x4 a = u32x4{l2[0], l2[1], h2[0], h2[1]};
@@ -326,14 +359,23 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
     if (kPipelined && moved) rescale();
     f32x4 sc[4][2];
     scores(sc);
-    if (kv0 + kBK > nk || (p.causal && kv0 + kBK - 1 > first_pos)) mask(sc, kv0);
+    const bool masked = kv0 + kBK > nk || (p.causal && kv0 + kBK - 1 > first_pos);
+    if (masked) mask(sc, kv0);
     u32x4 pb[2][2];
     if constexpr (kPipelined) {
       if (kv0 == 0) {
         moved = softmax(sc, pb, alpha);
       } else {
-        moved = softmax(sc, pb, alpha);
+        float ps[2];
+        const bool big = softmax_fixed(sc, pb, ps);
         pv(pbp, vb ^ 1);
+        if (__builtin_expect(big, 0)) {  // rare: a score passed the running max by more than 62: redo the tile with its max
+          moved = softmax(sc, pb, alpha);
+        } else {
+          l[0] += ps[0];
+          l[1] += ps[1];
+          moved = false;
+        }
       }
 #pragma unroll
       for (int k2 = 0; k2 < 2; ++k2) {
