@@ -230,6 +230,14 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
         sc[kt][1] = mfma_16x16x32(a, qop[1][kc], sc[kt][1]);
       }
     }
+    // keep four fragment reads in flight ahead of the MFMAs that consume them
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
   };
   // The causal / length mask, only where the tile reaches past the first query's position or past the keys.
   auto mask = [&](f32x4 (&sc)[4][2], int kv0) {
