@@ -254,6 +254,69 @@ def bench_prefill(dev):
     return out
 
 
+def bench_reference_shapes(dev):
+    """The workloads the reference publishes per-layer GPU times for (nanovllm_voxcpm/kernels/prefill_attn.py:10-12,
+    kernels/short_attn.py:159-161; measured there on an NVIDIA A10): paged causal prefill of 44 sequences x 46 new
+    tokens over a 50-token cached prefix (bf16 output, and the fused int8 output), and the head-start step of 200
+    sequences x 7 tokens with no prefix. Inputs rotate through > 256 MB so the Infinity Cache cannot serve them; the
+    published reference figures ride along for comparison (different hardware)."""
+    import torch
+
+    from voxcpm2_arabic_dialects_turbo_amd.ops import varlen_attention
+
+    out = {}
+    # 44 x 46 new tokens over a 50-token prefix, paged (256-token blocks, one block per sequence)
+    B, NEW, PRE = 44, 46, 50
+    nk = NEW + PRE
+    gq = torch.Generator(device=dev).manual_seed(60)
+    set_bytes = B * NEW * H * D * 2 + B * BS * HK * D * 2 * 2
+    n_sets = max(2, (300 << 20) // set_bytes + 1)
+    pool = n_sets * B
+    kc = torch.randn(pool, BS, HK, D, generator=gq, device=dev).to(torch.bfloat16)
+    vc = torch.randn(pool, BS, HK, D, generator=gq, device=dev).to(torch.bfloat16)
+    perm = torch.randperm(pool, generator=torch.Generator().manual_seed(61)).to(torch.int32)
+    tables = perm.view(n_sets, B, 1).to(dev)
+    qs = torch.randn(n_sets, B * NEW, H, D, generator=gq, device=dev).to(torch.bfloat16)
+    cu_q = torch.arange(0, B * NEW + 1, NEW, dtype=torch.int32, device=dev)
+    cu_k = torch.arange(0, B * nk + 1, nk, dtype=torch.int32, device=dev)
+    o = torch.empty(B * NEW, H, D, dtype=torch.bfloat16, device=dev)
+
+    def run_paged(quant):
+        def fn():
+            for i in range(n_sets):
+                varlen_attention(qs[i], None, None, cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, max_seqlen_q=NEW,
+                                 softmax_scale=SCALE, causal=True, block_table=tables[i], k_cache=kc, v_cache=vc,
+                                 out=None if quant else o, quant=quant)
+        return fn
+
+    for quant, key, ref in ((False, "paged_prefill_44x46_prefix50", {"fa2_a10_us": "70-76"}),
+                            (True, "paged_prefill_44x46_prefix50_int8", {"fa2_plus_quant_a10_us": 103,
+                                                                        "triton_fused_int8_a10_us": "66-74"})):
+        ms = _graph_ms(run_paged(quant), 20) / n_sets
+        flops, nbytes = prefill_units([NEW] * B, [nk] * B)
+        out[key] = dict(launch_us=round(ms * 1e3, 2), tflops=round(flops / (ms * 1e-3) / 1e12, 2),
+                        reference_published=ref)
+    del kc, vc, qs
+    # head-start step: 200 sequences x 7 tokens, packed, no prefix
+    B2, L2 = 200, 7
+    T2 = B2 * L2
+    set2 = T2 * (H + 2 * HK) * D * 2
+    n2 = max(2, (300 << 20) // set2 + 1)
+    qkv = torch.randn(n2, T2, (H + 2 * HK) * D, generator=gq, device=dev).to(torch.bfloat16)
+    cu2 = torch.arange(0, T2 + 1, L2, dtype=torch.int32, device=dev)
+    o2 = torch.empty(T2, H, D, dtype=torch.bfloat16, device=dev)
+
+    def run_head():
+        for i in range(n2):
+            q, k, v = qkv[i].split([H * D, HK * D, HK * D], dim=-1)
+            varlen_attention(q.view(T2, H, D), k.view(T2, HK, D), v.view(T2, HK, D), cu_seqlens_q=cu2,
+                             cu_seqlens_k=cu2, max_seqlen_q=L2, softmax_scale=SCALE, causal=True, out=o2)
+
+    ms2 = _graph_ms(run_head, 20) / n2
+    out["headstart_200x7"] = dict(launch_us=round(ms2 * 1e3, 2), reference_published={"fa2_a10_us": 113})
+    return out
+
+
 def bench_kv_copy(dev):
     """copy_kv_block_prefix over the model's cache layout (36 causal layers x K/V, 256-slot blocks): the voice-cloning
     prefix copy (44 entries x 50 tokens) and full-block copies (64 entries x 256 tokens); GB/s of bytes read and
@@ -387,6 +450,7 @@ def main():
     }
     if not args.decode_only:
         line["prefill"] = bench_prefill(dev)
+        line["prefill"]["reference_shapes"] = bench_reference_shapes(dev)
         line["kv_block_prefix_copy"] = bench_kv_copy(dev)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(res["workload"], args.cpu_seconds)
