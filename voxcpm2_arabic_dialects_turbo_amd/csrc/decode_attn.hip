@@ -191,7 +191,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
 #pragma unroll
       for (int kq = 0; kq < 4; ++kq) qv[kq] = ld_g16(qb + kq * 32);
     }
-    wait_vmem_all();  // the query is complete before the tile loop, whose waits then count tile loads only
 
     // the score MFMA's B operands for the segment: block-diagonal over (kv head, d)
     u32x4 qop[TT::KC];

@@ -8,6 +8,8 @@
 // Each lane moves 16 bytes with one dwordx4 load and one dwordx4 store, so a wave stores two full, aligned 512-byte
 // cache rows per instruction. Work is flattened over (token, tensor, 16-byte piece) so any row width that is a
 // multiple of 8 elements is covered, and a grid-stride loop keeps the grid small for large N.
+#include <type_traits>
+
 #include "vox_common.h"
 
 namespace vox {
@@ -24,21 +26,29 @@ __global__ __launch_bounds__(256) void store_kvcache_kernel(const uint16_t* __re
   const int64_t total = n * 2 * (int64_t)pieces;
   for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t tok = idx / (2 * pieces);
-    const int rem = (int)(idx - tok * 2 * pieces);
+    int64_t tok;
+    int rem;
+    if (total <= 0x7fffffff) {  // 32-bit index arithmetic whenever it fits (every real step)
+      const int i32 = (int)idx;
+      tok = i32 / (2 * pieces);
+      rem = i32 - (int)tok * 2 * pieces;
+    } else {
+      tok = idx / (2 * pieces);
+      rem = (int)(idx - tok * 2 * pieces);
+    }
     const int which = rem >= pieces;  // 0: key, 1: value
     const int piece = rem - which * pieces;
+    // The source row and the slot load together (the row index is always valid), so the copy costs one round trip.
+    const uint16_t* src = (which ? v + tok * v_row_stride : k + tok * k_row_stride) + piece * VEC;
+    typedef typename std::conditional<VEC == 8, u32x4, uint16_t>::type Unit;
+    const Unit val = *reinterpret_cast<const Unit*>(src);
     const int64_t slot = slot_mapping[tok];
+    asm volatile("" ::"v"(val), "v"(slot));  // keeps the row load ahead of the branch below (not sunk into it)
     // -1 marks a padded row (graph-captured batches); the range check keeps a bad slot from writing outside the
     // cache (the reference would write out of bounds there).
     if (slot < 0 || slot >= num_slots) continue;
-    const uint16_t* src = (which ? v + tok * v_row_stride : k + tok * k_row_stride) + piece * VEC;
     uint16_t* dst = (which ? v_cache : k_cache) + slot * row_elems + piece * VEC;
-    if constexpr (VEC == 8) {
-      *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
-    } else {
-      *dst = *src;
-    }
+    *reinterpret_cast<Unit*>(dst) = val;
   }
 }
 
