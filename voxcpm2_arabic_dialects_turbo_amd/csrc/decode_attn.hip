@@ -73,6 +73,14 @@ __device__ __forceinline__ void load_tile(Tile<HK>& T, const DecodeArgs& p, int6
   for (int i = 0; i < TT::VP; ++i) T.v[i] = ld_g16(vb + i * 1024);
 }
 
+// floor((a * b + c) / d) for the step-range bounds (all operands >= 0, d > 0): one 32-bit division when the
+// numerator fits in 32 bits, as it does for every real step, instead of the long 64-bit sequence.
+__device__ __forceinline__ int64_t muldiv(int64_t a, int64_t b, int64_t c, int64_t d) {
+  const uint64_t num = (uint64_t)a * (uint64_t)b + (uint64_t)c;
+  if (num <= 0xffffffffull && d <= 0xffffffffll) return (uint32_t)num / (uint32_t)d;
+  return (int64_t)(num / (uint64_t)d);
+}
+
 // A value every lane of the wave holds, moved to a scalar register (LDS reads land in vector registers).
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
@@ -143,8 +151,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
 
   // this workgroup's range [r, r1) and the sequence holding its first step: the last b with s_start[b] <= r
   // (an empty sequence shares its start with the next one, so the last such b is not empty)
-  const int r1 = (int)((int64_t)(g + 1) * S / G);
-  int r = (int)((int64_t)g * S / G);
+  const int r1 = (int)muldiv(g + 1, S, 0, G);
+  int r = (int)muldiv(g, S, 0, G);
   int b = 0;
   if (r < r1) {
     int lo = 0, hi = p.batch;  // s_start[lo] <= r < s_start[hi]
@@ -375,8 +383,8 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs p) {
     return;
   }
   const int64_t G = p.grid;
-  const int g_first = (int)(((sb + 1) * G + S - 1) / S) - 1;
-  const int g_last = (int)min(G - 1, (eb * G + S - 1) / S - 1);
+  const int g_first = (int)muldiv(sb + 1, G, S - 1, S) - 1;
+  const int g_last = (int)min(G - 1, muldiv(eb, G, S - 1, S) - 1);
   if (g_first >= g_last) return;  // one workgroup held the whole sequence and wrote it
 
   float M2 = -INFINITY, L2 = 0.f;
@@ -389,7 +397,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs p) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int64_t gg = min(g0 + u, g_last);
-      const bool live = g0 + u <= g_last && (gg * S / G) < ((gg + 1) * S / G);  // an empty range wrote nothing
+      const bool live = g0 + u <= g_last && muldiv(gg, S, 0, G) < muldiv(gg + 1, S, 0, G);  // empty: wrote nothing
       const float* pc = p.partials + (b + gg) * kPartialFloats;
       mc[u] = live ? pc[kMaxHeads * kD + hh] : -INFINITY;
       lc[u] = live ? pc[kMaxHeads * kD + kMaxHeads + hh] : 0.f;
