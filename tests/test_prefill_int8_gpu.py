@@ -103,3 +103,27 @@ def test_paged_int8_one_kv_head_and_zero_length_rows():
                                   max(nq), SCALE, quant=True)
     want = ref.varlen(q.float(), cu_q, cu_k, k_cache=kc, v_cache=vc, block_tables=tables)
     _check(out, want, "HK=1 paged int8")
+
+
+def test_int8_codes_round_half_to_even_at_exact_ties():
+    """One key per sequence and a zero query make p = exp2(0) = 1 and o = v exactly; with one element 127 per token
+    the scale is exactly 1, so the codes are rint(v) for values placed on half-integers (2.5 -> 2, -3.5 -> -4,
+    0.5 -> 0, ...): round half to even, the oracle's torch.round, bit-exact."""
+    gen = torch.Generator().manual_seed(74)
+    B = 12
+    ties = torch.tensor([0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5, -3.5, 10.5, -10.5, 126.5, -126.5])
+    v = ties[torch.randint(0, ties.numel(), (B, HK, D), generator=gen)]
+    v[:, 0, 0] = 127.0  # the token's max |o| over all heads: scale = 127 / 127 = 1
+    q, k = torch.zeros(B, H, D, dtype=torch.bfloat16), randn(gen, B, HK, D)
+    cu = torch.arange(B + 1, dtype=torch.int32)
+    out_q, scale = varlen_attention(q.to(DEV), k.to(DEV), v.to(torch.bfloat16).to(DEV), cu_seqlens_q=cu.to(DEV),
+                                    cu_seqlens_k=cu.to(DEV), max_seqlen_q=1, softmax_scale=SCALE, causal=True,
+                                    quant=True)
+    want = v.repeat_interleave(H // HK, dim=1).reshape(B, H * D)  # o of head h is v of its kv head
+    q_ref, s_ref = ref.quantize_rows(want.float())
+    assert torch.equal(scale.cpu(), s_ref) and float(s_ref[0]) == 1.0
+    assert torch.equal(out_q.cpu(), q_ref), "codes differ from round-half-to-even"
+    flat_v, flat_q = want.flatten(), out_q.cpu().flatten()
+    for val, code in ((2.5, 2), (-3.5, -4), (0.5, 0), (-1.5, -2), (126.5, 126)):
+        hit = flat_v == val
+        assert bool(hit.any()) and bool((flat_q[hit] == code).all()), f"{val} -> {code}"

@@ -430,14 +430,22 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
     for (int rt = 0; rt < 2; ++rt) {
       if (!row_ok[rt]) continue;
       const float scale = fmaxf(__uint_as_float(s_amax[(w * 32 + rt * 16 + r16) / g_rows]), 1e-6f) / 127.f;
+      // rint(o / scale) without a division per element: x = o * (1 / scale) is within 2.5e-5 of the exact
+      // quotient (|o / scale| <= 127.5, two roundings), so rint(x) is rint(o / scale) unless x lies within 1e-4 of
+      // a half-integer; those rare elements take the division. Same codes as dividing every element.
+      const float rs = 1.f / scale;
       int8_t* op = p.out_q + (int64_t)(q0 + tq_of[rt]) * p.out_row_stride + (int64_t)h_of[rt] * kD + jq * 4;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         const f32x4 o = acc[dt][rt];
         uint32_t packed = 0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          packed |= (uint32_t)(uint8_t)(int8_t)(int)__builtin_rintf(o[e] / scale) << (8 * e);
+        for (int e = 0; e < 4; ++e) {
+          const float x = o[e] * rs;
+          float r = __builtin_rintf(x);
+          if (__builtin_expect(fabsf(fabsf(x - r) - 0.5f) < 1e-4f, 0)) r = __builtin_rintf(o[e] / scale);
+          packed |= (uint32_t)(uint8_t)(int8_t)(int)r << (8 * e);
+        }
         *reinterpret_cast<uint32_t*>(op + dt * 16) = packed;
       }
     }
