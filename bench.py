@@ -314,6 +314,25 @@ def bench_reference_shapes(dev):
 
     ms2 = _graph_ms(run_head, 20) / n2
     out["headstart_200x7"] = dict(launch_us=round(ms2 * 1e3, 2), reference_published={"fa2_a10_us": 113})
+    del qkv
+    # non-causal short rows (kernels/short_attn.py:1-10, 70-90): LocDiT 11 tokens and LocEnc 5 tokens per stream,
+    # one stream per sequence of the 150-sequence decode batch; bf16 and the fused int8 output
+    from voxcpm2_arabic_dialects_turbo_amd.kernels.short_attn import short_attention
+
+    for name, L in (("locdit_150x11", 11), ("locenc_150x5", 5)):
+        Bs = 150
+        per = Bs * L * (H + 2 * HK) * D * 2
+        ns = max(2, (300 << 20) // per + 1)
+        qkv = torch.randn(ns, Bs, L, H + 2 * HK, D, generator=gq, device=dev).to(torch.bfloat16)
+        for quant in (False, True):
+            def run_short():
+                for i in range(ns):
+                    q, k, v = qkv[i].split([H, HK, HK], dim=2)
+                    short_attention(q, k, v, SCALE, quant=quant)
+
+            ms3 = _graph_ms(run_short, 20) / ns
+            out[name + ("_int8" if quant else "")] = dict(launch_us=round(ms3 * 1e3, 2))
+        del qkv
     return out
 
 
