@@ -152,3 +152,42 @@ def test_with_kvcache_entry_point_shapes():
     want = ref.varlen(q3.reshape(9, H, D).float(), [0, 3, 6, 9], [0, 40, 340, 597], k_cache=kc, v_cache=vc,
                       block_tables=tables)
     attn_close(out3.reshape(9, H, D), want, "with_kvcache Lq=3")
+
+
+def test_decode_closed_forms_identical_keys_and_one_token():
+    """Closed forms that pin the kernel without the oracle: with every key of a sequence identical the softmax is
+    uniform and o = mean(V) over the context; with a one-token context o = V[0] exactly (p = 1)."""
+    gen = torch.Generator().manual_seed(39)
+    lens = [1, 300, 513, 64]
+    kc, vc, tables = paged_pool(gen, lens, 40)
+    key = randn(gen, HK, D)
+    for b, n in enumerate(lens):  # the same key in every slot a sequence uses
+        for j in range(n):
+            blk, off = tables[b, j // BLOCK].item(), j % BLOCK
+            kc[blk, off] = key
+    q = randn(gen, len(lens), H, D)
+    out = decode_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), torch.tensor(lens, dtype=torch.int32, device=DEV),
+                           tables.to(DEV), SCALE).float().cpu()
+    for b, n in enumerate(lens):
+        rows = torch.stack([vc[tables[b, j // BLOCK], j % BLOCK] for j in range(n)]).float()  # [n, HK, D]
+        want = rows.mean(0).repeat_interleave(H // HK, dim=0)  # head h reads kv head h // 8
+        err = (out[b] - want).abs().max().item()
+        assert err <= (0.0 if n == 1 else 2e-2), f"sequence {b} (ctx {n}): max-abs {err}"
+
+
+def test_decode_equals_varlen_prefill_with_one_query():
+    """A decode step and a paged varlen call with one query per sequence (nq = 1, nk = ctx) compute the same
+    attention on different kernels; they agree within the attention tolerance."""
+    from voxcpm2_arabic_dialects_turbo_amd.ops import flash_attn_varlen_func
+
+    gen = torch.Generator().manual_seed(40)
+    lens = uniform_lens(gen, 24, 1, 1800)
+    kc, vc, tables = paged_pool(gen, lens, 200)
+    q = randn(gen, len(lens), H, D).to(DEV)
+    kc_d, vc_d, t_d = kc.to(DEV), vc.to(DEV), tables.to(DEV)
+    dec = decode_attention(q, kc_d, vc_d, torch.tensor(lens, dtype=torch.int32, device=DEV), t_d, SCALE)
+    cu_q = torch.arange(len(lens) + 1, dtype=torch.int32, device=DEV)
+    cu_k = torch.tensor([0] + np.cumsum(lens).tolist(), dtype=torch.int32, device=DEV)
+    pre = flash_attn_varlen_func(q, kc_d, vc_d, 1, cu_q, max(lens), cu_k, softmax_scale=SCALE, causal=True,
+                                 block_table=t_d)
+    attn_close(dec.float().cpu(), pre.float().cpu(), "decode vs varlen nq=1")
