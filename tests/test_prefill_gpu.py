@@ -188,3 +188,24 @@ def test_long_sequences_compute_bound_shape():
     out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), max(lens), _cu(lens).to(DEV), max(lens),
                                  _cu(lens).to(DEV), softmax_scale=SCALE, causal=True)
     attn_close(out, ref.varlen(q.float(), _cu(lens), _cu(lens), k=k, v=v), "long causal")
+
+
+def test_prefill_closed_forms_identical_keys():
+    """With every key of a sequence identical the causal softmax is uniform over the visible keys: query i of a
+    packed sequence gets mean(V[0..i]); query 0 gets V[0] exactly (one visible key, p = 1)."""
+    gen = torch.Generator().manual_seed(57)
+    lens = [1, 70, 200]
+    T = sum(lens)
+    q, v = randn(gen, T, H, D), randn(gen, T, HK, D)
+    k = randn(gen, 1, HK, D).expand(T, HK, D).contiguous()
+    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), max(lens), _cu(lens).to(DEV), max(lens),
+                                 _cu(lens).to(DEV), softmax_scale=SCALE, causal=True).float().cpu()
+    at = 0
+    for n in lens:
+        vs = v[at:at + n].float()
+        want = (vs.cumsum(0) / torch.arange(1, n + 1).view(n, 1, 1)).repeat_interleave(H // HK, dim=1)
+        got = out[at:at + n]
+        assert torch.equal(got[0], vs[0].repeat_interleave(H // HK, dim=0)), "query 0 must return V[0] exactly"
+        err = (got - want).abs().max().item()
+        assert err <= 2e-2, f"sequence of {n}: max-abs {err}"
+        at += n
