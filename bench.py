@@ -1,7 +1,7 @@
 #!/usr/bin/env python
 """Benchmark of the paged-KV attention path on one MI355X.
 
-Headline (``value``): BASELINE config 4, paged decode at peak concurrency across a 28-layer stack. One step = the 28
+Headline (``value``): benchmark config 4, paged decode at peak concurrency across a 28-layer stack. One step = the 28
 layers' ``Attention.forward`` decode calls (KV store of the new token + split-KV paged decode) for 150 sequences
 with contexts U[256, 2048], 16 query / 2 KV heads, head_dim 128, bf16, 256-token blocks; each layer has its own
 [2048, 256, 2, 128] K and V planes and its own q, seeded independently; the block tables (non-overlapping ids from a
@@ -9,7 +9,7 @@ shuffled 2048-block pool) are shared by the layers, as an engine's are. The step
 replayed, as the reference engine runs its decode step. ``value`` = algorithmic bytes of the step / step time.
 
 Beside it: the decode kernel's roofline (average launch duration from a graph of the 28 decode launches, HIP
-events on the launch stream), the prefill metric on BASELINE config 2 (varlen causal prefill, TFLOP/s against the
+events on the launch stream), the prefill metric on benchmark config 2 (varlen causal prefill, TFLOP/s against the
 bf16 dense MFMA peak, inputs rotated through > 256 MB so the Infinity Cache cannot serve them) plus a compute-bound
 supplementary prefill shape, and the CPU baseline: the oracle's torch path on the host cores over a bounded sample of
 the same decode workload.
@@ -97,7 +97,7 @@ def prefill_units(nq, nk):
 # ---------------------------------------------------------------------------------------------------------------------
 
 class DecodeWorkload:
-    """150 sequences x 28 layers, contexts U[256, 2048]."""
+    """Benchmark config 4: 150 sequences x 28 layers, contexts U[256, 2048]."""
 
     B, LAYERS, POOL = 150, 28, 2048
 
@@ -186,7 +186,7 @@ def bench_decode(args, dev):
 
 
 def bench_prefill(dev):
-    """BASELINE config 2 prefill (packed causal varlen, production's no-prefix path) and a supplementary
+    """Benchmark config 2 prefill (packed causal varlen, production's no-prefix path) and a supplementary
     compute-bound shape; per-launch ms from graphs of launches rotating over input sets."""
     import torch
 

@@ -12,7 +12,7 @@ Cases (shapes from the reference tests, tests/test_kernel_references.py):
   8 pages of 256; causal, bottom-right aligned; all 16 heads stored.
 - ``short_causal`` (:210-228): packed lens [1, 7, 16, 32, 3], causal over own tokens; heads 0, 7, 8, 15 stored.
 - ``dense`` (:229-237): B = 6, L = 5, non-causal; heads 0, 7, 8, 15 stored.
-- ``decode_c1``: 1 sequence, context 512, 4 blocks in random order, fp32.
+- ``decode_c1`` (benchmark config 1): 1 sequence, context 512, 4 blocks in random order, fp32.
 
 Run: python tests/golden/make_golden.py
 """

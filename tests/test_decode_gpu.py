@@ -29,7 +29,7 @@ def _check(q, kc, vc, lens, tables, what, h=H, hk=HK):
 
 
 def test_decode_config1_golden():
-    """BASELINE config 1 (1 sequence, context 512, 4 shuffled blocks), inputs rounded to bf16 on the GPU."""
+    """benchmark config 1 (1 sequence, context 512, 4 shuffled blocks), inputs rounded to bf16 on the GPU."""
     inp = make_golden.inputs("decode_c1")
     g = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden.npz"), allow_pickle=False)
     q, kc, vc = inp["q"].bfloat16(), inp["k_cache"].bfloat16(), inp["v_cache"].bfloat16()
@@ -38,7 +38,7 @@ def test_decode_config1_golden():
 
 
 def test_decode_config3_shape():
-    """40 sequences, contexts U[200, 1500], 1024-block pool."""
+    """benchmark config 3: 40 sequences, contexts U[200, 1500], 1024-block pool."""
     gen = torch.Generator().manual_seed(30)
     lens = uniform_lens(gen, 40, 200, 1500)
     kc, vc, tables = paged_pool(gen, lens, 1024)
@@ -129,7 +129,7 @@ def test_decode_batch_beyond_one_launch():
 
 
 def test_decode_config4_layer_full_size():
-    """BASELINE config 4, one layer at full size: 150 sequences, contexts U[256, 2048], 2048-block pool."""
+    """benchmark config 4, one layer at full size: 150 sequences, contexts U[256, 2048], 2048-block pool."""
     gen = torch.Generator().manual_seed(100)
     lens = uniform_lens(gen, 150, 256, 2048)
     kc, vc, tables = paged_pool(gen, lens, 2048)

@@ -79,7 +79,7 @@ def test_dense_golden():
 
 @pytest.mark.parametrize("mode", ["packed", "paged"])
 def test_config2_store_then_prefill(mode):
-    """8 sequences of U[64, 512] tokens packed by cu_seqlens; K/V stored into 256-token blocks of
+    """benchmark config 2: 8 sequences of U[64, 512] tokens packed by cu_seqlens; K/V stored into 256-token blocks of
     a 512-block pool, then causal prefill over the step's own k / v (packed) or through the block tables (paged)."""
     gen = torch.Generator().manual_seed(50)
     lens = uniform_lens(gen, 8, 64, 512)
@@ -103,7 +103,7 @@ def test_config2_store_then_prefill(mode):
 
 
 def test_config5_mixed_prefill_and_decode_rows():
-    """one varlen paged call with 6 new prefills (U[300, 600] tokens, stored first) and 120 decode
+    """benchmark config 5: one varlen paged call with 6 new prefills (U[300, 600] tokens, stored first) and 120 decode
     rows (one query over U[128, 1800] cached tokens), 2048-block pool."""
     gen = torch.Generator().manual_seed(51)
     pre = uniform_lens(gen, 6, 300, 600)

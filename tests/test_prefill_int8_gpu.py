@@ -76,7 +76,7 @@ def test_short_non_causal_int8(L):
 
 
 def test_config2_packed_int8_with_smoothing():
-    """BASELINE config 2 shape (8 packed causal sequences, L ~ U[64, 512]), int8 output with inv_smooth."""
+    """benchmark config 2 shape (8 packed causal sequences, L ~ U[64, 512]), int8 output with inv_smooth."""
     gen = torch.Generator().manual_seed(72)
     lens = uniform_lens(gen, 8, 64, 512)
     T = sum(lens)

@@ -37,7 +37,7 @@ def _qkv_views(gen, n):
 
 
 def test_store_config2_shape_strided_rows_bit_exact():
-    """~2304 prefill tokens of 8 sequences scattered into 256-token blocks of a 512-block pool."""
+    """benchmark config 2: ~2304 prefill tokens of 8 sequences scattered into 256-token blocks of a 512-block pool."""
     gen = torch.Generator().manual_seed(20)
     lens = torch.randint(64, 513, (8,), generator=gen).tolist()
     _, _, tables = paged_pool(gen, lens, 512)
