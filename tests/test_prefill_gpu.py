@@ -209,3 +209,34 @@ def test_prefill_closed_forms_identical_keys():
         err = (got - want).abs().max().item()
         assert err <= 2e-2, f"sequence of {n}: max-abs {err}"
         at += n
+
+
+def test_prefill_scores_growing_across_key_tiles():
+    """Later key tiles score far above the first (log2-scaled scores hundreds of units higher), which sends those
+    tiles down the recompute-with-their-max path of the softmax; the result still matches the oracle, with no
+    overflow, for packed and paged keys."""
+    gen = torch.Generator().manual_seed(58)
+    L = 300
+    u = torch.randn(HK, D, generator=gen)  # a direction per kv group; every query leans along its group's
+    q = (u.repeat_interleave(H // HK, dim=0).expand(L, H, D) + 0.3 * torch.randn(L, H, D, generator=gen))
+    q = q.to(torch.bfloat16)
+    k = randn(gen, L, HK, D).float()
+    v = randn(gen, L, HK, D)
+    # keys 64.. point along u with growing magnitude: raw scores up to ~1500, each key tile ~50+ log2 units above
+    # the last
+    for j in range(64, L):
+        k[j] = u * (0.05 * (j - 63))
+    k = k.to(torch.bfloat16)
+    cu = _cu([L])
+    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), L, cu.to(DEV), L, cu.to(DEV), softmax_scale=SCALE,
+                                 causal=True)
+    want = ref.varlen(q.float(), cu, cu, k=k, v=v)
+    assert torch.isfinite(out.float()).all()
+    attn_close(out, want, "growing scores, packed")
+    kc, vc, tables = paged_pool(gen, [L], 4)
+    for j in range(L):
+        kc[tables[0, j // BLOCK], j % BLOCK] = k[j]
+        vc[tables[0, j // BLOCK], j % BLOCK] = v[j]
+    out2 = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), L, cu.to(DEV), L, cu.to(DEV),
+                                  softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
+    attn_close(out2, want, "growing scores, paged")
