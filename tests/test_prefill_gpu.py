@@ -240,3 +240,35 @@ def test_prefill_scores_growing_across_key_tiles():
     out2 = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), L, cu.to(DEV), L, cu.to(DEV),
                                   softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
     attn_close(out2, want, "growing scores, paged")
+
+
+@pytest.mark.parametrize("bs", [256, 32])
+def test_paged_unmapped_blocks_read_as_zeros_and_slots_past_the_keys_stay_unread(bs):
+    """Block-table entries that address no block (-1, or past the pool) read as zero keys and values, and cache slots
+    past a sequence's keys are never used: they hold NaN here, and the output stays finite and equal to the oracle's
+    over a cache in which those entries point at an all-zero block. 256: the tiles that go straight to LDS (range-
+    checked loads); 32: the register-staged per-piece path."""
+    gen = torch.Generator().manual_seed(71 + bs)
+    nq = [50, 3, 129]
+    nk = [50 + 600, 3 + 300, 129 + 40]
+    pool = sum((n + bs - 1) // bs for n in nk) + 2
+    kc, vc, tables = paged_pool(gen, nk, pool, block_size=bs)
+    for b, n in enumerate(nk):  # NaN in every slot past the sequence's keys
+        for j in range((n + bs - 1) // bs):
+            used = min(bs, n - j * bs)
+            kc[tables[b, j], used:] = float("nan")
+            vc[tables[b, j], used:] = float("nan")
+    zero_id = pool  # the oracle's all-zero block
+    kc_ref = torch.cat([kc, torch.zeros(1, bs, HK, D, dtype=kc.dtype)])
+    vc_ref = torch.cat([vc, torch.zeros(1, bs, HK, D, dtype=vc.dtype)])
+    t_ref = tables.clone()
+    t_gpu = tables.clone()
+    for b, j, bad in [(0, 1, -1), (1, 0, pool + 5), (2, 0, -7)]:  # one unmapped block per sequence
+        t_gpu[b, j] = bad
+        t_ref[b, j] = zero_id
+    q = randn(gen, sum(nq), H, D)
+    out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), max(nq), _cu(nq).to(DEV), max(nk),
+                                 _cu(nk).to(DEV), softmax_scale=SCALE, causal=True, block_table=t_gpu.to(DEV))
+    assert torch.isfinite(out.float()).all()
+    want = ref.varlen(q.float(), _cu(nq), _cu(nk), k_cache=kc_ref, v_cache=vc_ref, block_tables=t_ref)
+    attn_close(out, want, f"unmapped blocks, block_size {bs}")

@@ -38,6 +38,8 @@ constexpr int kRows = 128;       // query rows per workgroup
 // the transposed V reads are fastest from 152 up; the 16-byte staging writes do not care.
 constexpr int kKsStride = kD + 16;
 constexpr int kVsStride = kD + 24;
+// word 3 of a raw buffer descriptor (32-bit data format; offsets in bytes, range-checked against num_records)
+constexpr int kBufferWord3 = 0x00020000;
 
 // Where a workgroup's keys come from (one kernel instance each, so no path's loop-carried state constrains another's
 // load waits): packed [Tk, HK, D] rows; the paged cache with block_size a multiple of 64 (a 64-key tile lies in one
@@ -53,7 +55,7 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
 
   const int qt = blockIdx.x;
   const int b = blockIdx.y;
-  const int half = QUANT ? (int)(threadIdx.x >> 8) : 0;
+  const int half = QUANT ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8)) : 0;  // wave-uniform
   const int g = QUANT ? half : (int)blockIdx.z;
   auto& ks = ks_all[half];
   auto& vs2 = vs_all[half];
@@ -78,7 +80,7 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
   if (qt * BQ >= nq) return;
 
   const int tid = threadIdx.x & 255;  // thread within the half
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   if constexpr (QUANT)
     if (threadIdx.x < (unsigned)BQ) s_amax[threadIdx.x] = 0u;  // ordered before the atomics by the barriers below
   const int lane = tid & 63;
@@ -117,12 +119,9 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) acc[dt][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // ---- K/V tile loads: 4 + 4 pieces of 16 bytes per thread (piece i: key lrow + 16 i of the tile, dims dc .. dc + 8),
-  // unconditional and in bounds (a key past nk reads the tile's last real key or, in a paged tile, a slot of the same
-  // block; an unmapped block reads block 0; either is zeroed when staged). Packed keys and paged tiles that lie inside
-  // one cache block (block_size a multiple of 64) address a tile from one uniform base plus a 32-bit lane offset, with
-  // the tile's block id read one tile ahead; other block sizes read each piece's block id one tile ahead
-  // (fetch_bids), so a tile's eight loads still issue back to back.
+  // ---- K/V tile pieces: piece i of a tile is key lrow + 16 i, dims dc .. dc + 8 (16 bytes per thread). Packed keys
+  // and paged tiles inside one cache block (block_size a multiple of 64) go straight to LDS (the DMA path below);
+  // other block sizes read each piece's block id one tile ahead (fetch_bids) and stage through registers.
   constexpr bool paged = KV != kPacked;
   constexpr bool blk_tiles = KV == kPagedTiles;
   const int rs_k = paged ? HK * kD : (int)p.k_row_stride;  // elements between consecutive keys (< 2^24)
@@ -133,7 +132,6 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
   int bids[4] = {0, 0, 0, 0};  // per-piece block ids (paged, block_size not a multiple of 64)
   int tile_bid = 0;            // the block id of the next tile to load (paged, block_size a multiple of 64)
   unsigned live = 0;           // bit i: piece i is a real key
-  bool full = false;           // every key of the tile real: staged without the zero selects
   auto fetch_bids = [&](int kv0) {
     if constexpr (!paged) return;
     if constexpr (blk_tiles) {
@@ -146,33 +144,10 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
       bids[i] = p.block_tables[(int64_t)b * p.bt_stride + jc / p.block_size];
     }
   };
+  // register-staged loads (block sizes that are not a multiple of 64): unconditional and in bounds (a key past nk
+  // reads the sequence's last key, an unmapped block reads block 0; both are zeroed when staged)
   auto load_tile = [&](int kv0) {
-    const int lim = min(kBK, nk - kv0) - 1;  // the tile's last real key, relative (>= 0)
-    if constexpr (!paged || blk_tiles) {
-      const uint16_t* kb;
-      const uint16_t* vb;
-      bool okb = true;
-      if constexpr (!paged) {
-        kb = p.k_src + (int64_t)(k0 + kv0) * p.k_row_stride + g * kD;
-        vb = p.v_src + (int64_t)(k0 + kv0) * p.v_row_stride + g * kD;
-      } else {
-        okb = tile_bid >= 0 && tile_bid < p.num_blocks;
-        const int64_t row0 = (int64_t)(okb ? tile_bid : 0) * p.block_size + kv0 % p.block_size;
-        kb = p.k_cache + row0 * rs_k + g * kD;
-        vb = p.v_cache + row0 * rs_k + g * kD;
-      }
-      full = okb && lim == kBK - 1;
-      live = 0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = min(lrow + 16 * i, lim);
-        kr[i] = ld_g16(kb + (uint32_t)(r * rs_k + dc));
-        vr[i] = ld_g16(vb + (uint32_t)(r * rs_v + dc));
-        live |= (okb && lrow + 16 * i <= lim ? 1u : 0u) << i;
-      }
-    } else {
     live = 0;
-    full = false;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int jj = kv0 + lrow + 16 * i;
@@ -184,43 +159,22 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
       vr[i] = ld_g16(p.v_cache + off);
       live |= (ok ? 1u : 0u) << i;
     }
-    }
   };
   auto stage_tile = [&](int vb) {
     auto& vs = vs2[vb];
-    if (full) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int pc = tid + i * 256;
-        *reinterpret_cast<u32x4*>(&ks[pc >> 4][(pc & 15) * 8]) = kr[i];
-        *reinterpret_cast<u32x4*>(&vs[pc >> 4][(pc & 15) * 8]) = vr[i];
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int pc = tid + i * 256;
-        const bool ok = (live >> i) & 1u;
-        *reinterpret_cast<u32x4*>(&ks[pc >> 4][(pc & 15) * 8]) = ok ? kr[i] : zero4();
-        *reinterpret_cast<u32x4*>(&vs[pc >> 4][(pc & 15) * 8]) = ok ? vr[i] : zero4();
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int pc = tid + i * 256;
+      const bool ok = (live >> i) & 1u;
+      *reinterpret_cast<u32x4*>(&ks[pc >> 4][(pc & 15) * 8]) = ok ? kr[i] : zero4();
+      *reinterpret_cast<u32x4*>(&vs[pc >> 4][(pc & 15) * 8]) = ok ? vr[i] : zero4();
     }
   };
   // this lane's transposed-read address inside a 16-key x 16-d block: row jq*4 + r16/4, column 4*(r16%4)
   const int tr_off = (jq * 4 + (r16 >> 2)) * kVsStride + 4 * (r16 & 3);
   const int first_pos = nk - nq + qt * BQ;  // the position of the tile's first query token
 
-  if (kv_end > 0) {
-    fetch_bids(0);
-    load_tile(0);
-    fetch_bids(kBK);
-  }
-  // The query and the first tile arrive in one round trip; waiting here (rather than at the first use) also lets
-  // the compiler's wait analysis see the query registers complete at the loop head, so no wait inside the loop
-  // covers the prefetched tile.
-  wait_vmem_all();
-  // ---- per-tile steps. The loop is software-pipelined: P V of tile j - 1 (V from the other LDS buffer, P from
-  // registers) runs in the same instruction block as tile j's softmax, so its MFMAs and transposed reads interleave
-  // with the softmax VALU work; K is single-buffered (only tile j's scores read it).
+  // ---- per-tile steps of the register-staged path (padded LDS rows; V double-buffered, K single-buffered)
   auto scores = [&](f32x4 (&sc)[4][2]) {  // S^T[key][row] = K Q^T
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
@@ -345,9 +299,6 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
       }
   };
 
-  // The per-piece block-id path keeps eight more live registers; it runs the steps in order instead (no spills).
-  constexpr bool kPipelined = KV != kPagedPieces;
-  u32x4 pbp[2][2];  // P^T of the previous tile, waiting for its P V
   float alpha[2] = {1.f, 1.f};  // the last softmax's accumulator factors
   bool moved = false;           // ... and whether any of them is not 1
   auto rescale = [&]() {
@@ -357,30 +308,127 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
       acc[dt][1] *= alpha[1];
     }
   };
-  int vb = 0;       // LDS buffer of this tile's V
-  for (int kv0 = 0; kv0 < kv_end; kv0 += kBK) {
-    stage_tile(vb);
-    __syncthreads();
-    if (kv0 + kBK < kv_end) {  // in flight while this tile computes
-      load_tile(kv0 + kBK);
-      fetch_bids(kv0 + 2 * kBK);
-    }
-    // the previous tile's max move, now that its P V (which used the old max) is in the accumulators; done here
-    // rather than after the softmax so that no branch splits the softmax from the P V it interleaves with
-    if (kPipelined && moved) rescale();
-    f32x4 sc[4][2];
-    scores(sc);
-    const bool masked = kv0 + kBK > nk || (p.causal && kv0 + kBK - 1 > first_pos);
-    if (masked) mask(sc, kv0);
-    u32x4 pb[2][2];
-    if constexpr (kPipelined) {
+  constexpr bool kDma = KV != kPagedPieces;
+  if constexpr (kDma) {
+    // ---- direct-to-LDS tiles (packed keys; paged tiles inside one cache block) ----
+    // K and V tiles go from global memory straight into LDS (buffer_load_dwordx4 ... lds: lane i's 16 bytes land in
+    // slot i of a 1 KB run = four 256-byte rows), with no register staging, so the 32 registers a staged tile
+    // occupies are free for P V operand read-ahead. Both are double-buffered in separate arrays: the compiler can
+    // then tell a tile's reads from the next tile's in-flight writes and waits for those only at the barrier that
+    // ends the tile (one barrier per tile). Rows are 256 bytes, unpadded; bank conflicts are avoided by permuting the
+    // 16-byte chunks of a row instead: chunk c of row R sits in slot c ^ (R & 15) in K (a K-fragment read's 16 rows
+    // hit 16 different slots) and in slot c ^ 2 (R & 7) in V (the 8 rows under a transposed read's 32 lanes hit 16
+    // different slots). The permutation is applied on the global side: the lane that fills slot lc of row R fetches
+    // chunk lc ^ f(R).
+    constexpr int kTB = kBK * 256;  // bytes of one tile
+    __shared__ __attribute__((aligned(1024))) uint8_t kt0[NH][kTB];
+    __shared__ __attribute__((aligned(1024))) uint8_t kt1[NH][kTB];
+    __shared__ __attribute__((aligned(1024))) uint8_t vt0[NH][kTB];
+    __shared__ __attribute__((aligned(1024))) uint8_t vt1[NH][kTB];
+    const int lc = lane & 15;
+    const int fk = lrow & 15, fv = 2 * (lrow & 7);  // rows 16 i + lrow share these
+    const uint32_t dk_off = (uint32_t)((lrow * rs_k + ((lc ^ fk) << 3)) * 2);
+    const uint32_t dv_off = (uint32_t)((lrow * rs_v + ((lc ^ fv) << 3)) * 2);
+    typedef __attribute__((address_space(3))) void lvoid;
+    // Issues one tile's 4 + 4 DMA loads into (kd, vd); piece i of wave w fills rows 16 i + 4 w .. + 3. Each piece
+    // is a raw buffer load whose descriptor covers exactly the piece's real keys: keys past nk and a whole tile of
+    // an unmapped block read as zeros (the hardware's range check), so no address is clamped and no tile is
+    // patched. (The buffer form also keeps the compiler's LDS wait counting exact; the global form makes it wait
+    // for every LDS read to finish.)
+    auto dma = [&](uint8_t* kd, uint8_t* vd, int kv0) {
+      const char* kbc;
+      const char* vbc;
+      int nreal = min(kBK, nk - kv0);  // keys of this tile that exist
+      if constexpr (!paged) {
+        kbc = reinterpret_cast<const char*>(p.k_src + (int64_t)(k0 + kv0) * p.k_row_stride + g * kD);
+        vbc = reinterpret_cast<const char*>(p.v_src + (int64_t)(k0 + kv0) * p.v_row_stride + g * kD);
+      } else {
+        const bool okb = tile_bid >= 0 && tile_bid < p.num_blocks;
+        const int64_t row0 = (int64_t)(okb ? tile_bid : 0) * p.block_size + kv0 % p.block_size;
+        kbc = reinterpret_cast<const char*>(p.k_cache + row0 * rs_k + g * kD);
+        vbc = reinterpret_cast<const char*>(p.v_cache + row0 * rs_k + g * kD);
+        if (!okb) nreal = 0;
+      }
+      uint8_t* kdw = kd + w * 1024;
+      uint8_t* vdw = vd + w * 1024;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rows = min(max(nreal - 16 * i, 0), 16);  // real keys among the piece's 16 rows
+        const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbc + (int64_t)(16 * i) * rs_k * 2),
+                                                          (short)0, rows * rs_k * 2, kBufferWord3);
+        const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vbc + (int64_t)(16 * i) * rs_v * 2),
+                                                          (short)0, rows * rs_v * 2, kBufferWord3);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lvoid*)(kdw + i * 4096), 16, dk_off, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lvoid*)(vdw + i * 4096), 16, dv_off, 0, 0, 0);
+      }
+    };
+    // K fragment (rows kt*16 + r16, chunk kc*4 + jq) at byte kt*4096 + (krd0 ^ (kc << 6))
+    const uint32_t krd0 = (uint32_t)(r16 * 256 + ((jq ^ r16) << 4));
+    auto scores_d = [&](const uint8_t* kd, f32x4 (&sc)[4][2]) {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        sc[kt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+        sc[kt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) {
+          const u32x4 a = *reinterpret_cast<const u32x4*>(kd + kt * 4096 + (krd0 ^ (uint32_t)(kc << 6)));
+          sc[kt][0] = mfma_16x16x32(a, qop[0][kc], sc[kt][0]);
+          sc[kt][1] = mfma_16x16x32(a, qop[1][kc], sc[kt][1]);
+        }
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+      for (int i = 0; i < 12; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    };
+    // transposed V read for (dt, k2, half h): rows k2*32 + h*16 + jq*4 + r16/4, dims dt*16 + 4 (r16 & 3) .. + 3,
+    // at byte k2*8192 + h*4096 + (vrd0 ^ (dt << 5))
+    const int rl = jq * 4 + (r16 >> 2);
+    const uint32_t vrd0 = (uint32_t)(rl * 256 + ((rl & 7) << 5) + ((r16 & 3) << 3));
+    auto pv_read = [&](const uint8_t* vd, u32x4 (&va)[8][2]) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) {
+          const uint8_t* vp = vd + k2 * 8192 + (vrd0 ^ (uint32_t)(dt << 5));
+          const u32x2 lo = __builtin_bit_cast(u32x2, lds_read_tr16(reinterpret_cast<const uint16_t*>(vp)));
+          const u32x2 hi = __builtin_bit_cast(u32x2, lds_read_tr16(reinterpret_cast<const uint16_t*>(vp + 4096)));
+          va[dt][k2] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
+    };
+    auto pv_mfma = [&](const u32x4 (&va)[8][2], const u32x4 (&pbi)[2][2]) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) {
+          acc[dt][0] = mfma_16x16x32(va[dt][k2], pbi[k2][0], acc[dt][0]);
+          acc[dt][1] = mfma_16x16x32(va[dt][k2], pbi[k2][1], acc[dt][1]);
+        }
+    };
+    // one tile: the next tile's DMA goes out first, then the scores, the softmax and P V, whose transposed V reads run
+    // 16 ahead of the MFMAs that consume them (left alone, the compiler waits for each operand right after reading
+    // it); the next tile has landed by the barrier
+    auto step = [&](int kv0, const uint8_t* kc_, const uint8_t* vc_, uint8_t* kn, uint8_t* vn) {
+      const bool has_next = kv0 + kBK < kv_end;
+      if (has_next) {
+        dma(kn, vn, kv0 + kBK);
+        fetch_bids(kv0 + 2 * kBK);
+      }
+      f32x4 sc[4][2];
+      scores_d(kc_, sc);
+      const bool masked = kv0 + kBK > nk || (p.causal && kv0 + kBK - 1 > first_pos);
+      if (masked) mask(sc, kv0);
+      u32x4 pb[2][2];
       if (kv0 == 0) {
-        moved = softmax(sc, pb, alpha);
+        softmax(sc, pb, alpha);  // the accumulators are still zero: no rescale
+        moved = false;
       } else {
         float ps[2];
         const bool big = softmax_fixed(sc, pb, ps);
-        pv(pbp, vb ^ 1);
-        if (__builtin_expect(big, 0)) {  // rare: a score passed the running max by more than 62: redo the tile with its max
+        if (__builtin_expect(big, 0)) {  // rare: a score passed the running max by more than 62: redo with its max
           moved = softmax(sc, pb, alpha);
         } else {
           l[0] += ps[0];
@@ -388,21 +436,58 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
           moved = false;
         }
       }
+      if (__builtin_expect(moved, 0)) rescale();
+      u32x4 va[8][2];
+      pv_read(vc_, va);
+      pv_mfma(va, pb);
+      __builtin_amdgcn_sched_group_barrier(0x100, 16, 1);
 #pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2) {
-        pbp[k2][0] = pb[k2][0];
-        pbp[k2][1] = pb[k2][1];
+      for (int i = 0; i < 4; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
       }
-    } else {
+      __builtin_amdgcn_sched_group_barrier(0x008, 16, 1);
+      __syncthreads();  // the next tile has landed (the barrier waits for this wave's DMA) and this one is free
+    };
+    if (kv_end > 0) {
+      fetch_bids(0);
+      dma(kt0[half], vt0[half], 0);
+      fetch_bids(kBK);
+      wait_vmem_all();  // the query and tile 0
+      __syncthreads();
+      for (int kv0 = 0; kv0 < kv_end; kv0 += 2 * kBK) {
+        step(kv0, kt0[half], vt0[half], kt1[half], vt1[half]);
+        if (kv0 + kBK < kv_end) step(kv0 + kBK, kt1[half], vt1[half], kt0[half], vt0[half]);
+      }
+    }
+  } else {
+    if (kv_end > 0) {
+      fetch_bids(0);
+      load_tile(0);
+      fetch_bids(kBK);
+    }
+    // The query and the first tile arrive in one round trip; waiting here (rather than at the first use) also lets
+    // the compiler's wait analysis see the query registers complete at the loop head, so no wait inside the loop
+    // covers the prefetched tile.
+    wait_vmem_all();
+    int vb = 0;       // LDS buffer of this tile's V
+    for (int kv0 = 0; kv0 < kv_end; kv0 += kBK) {
+      stage_tile(vb);
+      __syncthreads();
+      if (kv0 + kBK < kv_end) {  // in flight while this tile computes
+        load_tile(kv0 + kBK);
+        fetch_bids(kv0 + 2 * kBK);
+      }
+      f32x4 sc[4][2];
+      scores(sc);
+      const bool masked = kv0 + kBK > nk || (p.causal && kv0 + kBK - 1 > first_pos);
+      if (masked) mask(sc, kv0);
+      u32x4 pb[2][2];
       if (softmax(sc, pb, alpha)) rescale();
       pv(pb, vb);
+      vb ^= 1;
+      __syncthreads();  // K and the previous V buffer are free for the next tile's staging
     }
-    vb ^= 1;
-    __syncthreads();  // K and the previous V buffer are free for the next tile's staging
-  }
-  if (kPipelined && kv_end > 0) {
-    if (moved) rescale();
-    pv(pbp, vb ^ 1);
   }
 
   if constexpr (QUANT) {
