@@ -197,17 +197,17 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
     __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
   };
   // The causal / length mask, only where the tile reaches past the first query's position or past the keys.
+  // Key j = kv0 + kt*16 + jq*4 + rr is kept when j < nk and (causal) j <= qpos: one limit per row, relative to the
+  // lane's first key, so each element costs a compare against a constant and a select.
   auto mask = [&](f32x4 (&sc)[4][2], int kv0) {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+    for (int rt = 0; rt < 2; ++rt) {
+      const int last = (p.causal ? min(nk - 1, qpos[rt]) : nk - 1) - (kv0 + jq * 4);
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int jj = kv0 + kt * 16 + jq * 4 + rr;
-          const bool ok = jj < nk && (!p.causal || jj <= qpos[rt]);
-          sc[kt][rt][rr] = ok ? sc[kt][rt][rr] : -INFINITY;
-        }
+        for (int rr = 0; rr < 4; ++rr) sc[kt][rt][rr] = kt * 16 + rr <= last ? sc[kt][rt][rr] : -INFINITY;
+    }
   };
   // Online softmax, one row per lane column, branch-free. The scale goes into the exp2 argument (one FMA); a row's
   // running max moves only when its tile max exceeds it by more than 8 in log2 units (p <= 256, exact after the
@@ -330,10 +330,10 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
     const uint32_t dk_off = (uint32_t)((lrow * rs_k + ((lc ^ fk) << 3)) * 2);
     const uint32_t dv_off = (uint32_t)((lrow * rs_v + ((lc ^ fv) << 3)) * 2);
     typedef __attribute__((address_space(3))) void lvoid;
-    // Issues one tile's 4 + 4 DMA loads into (kd, vd); piece i of wave w fills rows 16 i + 4 w .. + 3. Each piece
-    // is a raw buffer load whose descriptor covers exactly the piece's real keys: keys past nk and a whole tile of
-    // an unmapped block read as zeros (the hardware's range check), so no address is clamped and no tile is
-    // patched. (The buffer form also keeps the compiler's LDS wait counting exact; the global form makes it wait
+    // Issues one tile's 4 + 4 DMA loads into (kd, vd); piece i of wave w fills rows 16 i + 4 w .. + 3. In a tile
+    // with missing keys each piece is a raw buffer load whose descriptor covers exactly the piece's real keys: keys
+    // past nk and a whole tile of an unmapped block read as zeros (the hardware's range check), so no address is
+    // clamped and no tile is patched. (The buffer form also keeps the compiler's LDS wait counting exact; the global form makes it wait
     // for every LDS read to finish.)
     auto dma = [&](uint8_t* kd, uint8_t* vd, int kv0) {
       const char* kbc;
@@ -351,15 +351,25 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
       }
       uint8_t* kdw = kd + w * 1024;
       uint8_t* vdw = vd + w * 1024;
+      if (nreal == kBK) {  // every key real: one descriptor per tile, the piece offset in the scalar offset
+        const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbc), (short)0, kBK * rs_k * 2, kBufferWord3);
+        const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vbc), (short)0, kBK * rs_v * 2, kBufferWord3);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int rows = min(max(nreal - 16 * i, 0), 16);  // real keys among the piece's 16 rows
-        const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbc + (int64_t)(16 * i) * rs_k * 2),
-                                                          (short)0, rows * rs_k * 2, kBufferWord3);
-        const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vbc + (int64_t)(16 * i) * rs_v * 2),
-                                                          (short)0, rows * rs_v * 2, kBufferWord3);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lvoid*)(kdw + i * 4096), 16, dk_off, 0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lvoid*)(vdw + i * 4096), 16, dv_off, 0, 0, 0);
+        for (int i = 0; i < 4; ++i) {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lvoid*)(kdw + i * 4096), 16, dk_off, 16 * i * rs_k * 2, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lvoid*)(vdw + i * 4096), 16, dv_off, 16 * i * rs_v * 2, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int rows = __builtin_amdgcn_readfirstlane(min(max(nreal - 16 * i, 0), 16));  // real keys in the piece
+          const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbc + (int64_t)(16 * i) * rs_k * 2),
+                                                            (short)0, rows * rs_k * 2, kBufferWord3);
+          const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vbc + (int64_t)(16 * i) * rs_v * 2),
+                                                            (short)0, rows * rs_v * 2, kBufferWord3);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lvoid*)(kdw + i * 4096), 16, dk_off, 0, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lvoid*)(vdw + i * 4096), 16, dv_off, 0, 0, 0);
+        }
       }
     };
     // K fragment (rows kt*16 + r16, chunk kc*4 + jq) at byte kt*4096 + (krd0 ^ (kc << 6))
@@ -376,13 +386,13 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
           sc[kt][1] = mfma_16x16x32(a, qop[1][kc], sc[kt][1]);
         }
       }
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
 #pragma unroll
-      for (int i = 0; i < 12; ++i) {
+      for (int i = 0; i < 8; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
     };
     // transposed V read for (dt, k2, half h): rows k2*32 + h*16 + jq*4 + r16/4, dims dt*16 + 4 (r16 & 3) .. + 3,
     // at byte k2*8192 + h*4096 + (vrd0 ^ (dt << 5))
