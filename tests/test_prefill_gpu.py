@@ -272,3 +272,23 @@ def test_paged_unmapped_blocks_read_as_zeros_and_slots_past_the_keys_stay_unread
     assert torch.isfinite(out.float()).all()
     want = ref.varlen(q.float(), _cu(nq), _cu(nk), k_cache=kc_ref, v_cache=vc_ref, block_tables=t_ref)
     attn_close(out, want, f"unmapped blocks, block_size {bs}")
+
+
+def test_large_ragged_grid_in_per_xcd_order():
+    """A grid of 128 q tiles x 8 sequences x 2 kv heads (>= 1024 workgroups: the launcher deals contiguous work
+    ranges per XCD) with ragged lengths, so most ranges mix empty and full q tiles; packed and paged keys."""
+    gen = torch.Generator().manual_seed(74)
+    lens = [2048, 100, 1500, 7, 900, 2047, 64, 1300]
+    T = sum(lens)
+    q, k, v = randn(gen, T, H, D), randn(gen, T, HK, D), randn(gen, T, HK, D)
+    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), max(lens), _cu(lens).to(DEV), max(lens),
+                                 _cu(lens).to(DEV), softmax_scale=SCALE, causal=True)
+    want = ref.varlen(q.float(), _cu(lens), _cu(lens), k=k, v=v)
+    attn_close(out, want, "per-XCD order, packed")
+    nq = [max(1, n // 3) for n in lens]  # new tokens over cached prefixes
+    kc, vc, tables = paged_pool(gen, lens, sum((n + BLOCK - 1) // BLOCK for n in lens) + 4)
+    qp = randn(gen, sum(nq), H, D)
+    outp = flash_attn_varlen_func(qp.to(DEV), kc.to(DEV), vc.to(DEV), max(nq), _cu(nq).to(DEV), max(lens),
+                                  _cu(lens).to(DEV), softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
+    wantp = ref.varlen(qp.float(), _cu(nq), _cu(lens), k_cache=kc, v_cache=vc, block_tables=tables)
+    attn_close(outp, wantp, "per-XCD order, paged")

@@ -127,3 +127,16 @@ def test_int8_codes_round_half_to_even_at_exact_ties():
     for val, code in ((2.5, 2), (-3.5, -4), (0.5, 0), (-1.5, -2), (126.5, 126)):
         hit = flat_v == val
         assert bool(hit.any()) and bool((flat_q[hit] == code).all()), f"{val} -> {code}"
+
+
+def test_int8_large_ragged_grid_in_per_xcd_order():
+    """int8 output on a grid of 128 q tiles x 8 sequences (>= 1024 workgroups: per-XCD work order) with ragged
+    lengths."""
+    gen = torch.Generator().manual_seed(75)
+    lens = [2048, 33, 1200, 700, 5, 1999, 64, 1500]
+    T = sum(lens)
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32)
+    q, k, v = randn(gen, T, H, D), randn(gen, T, HK, D), randn(gen, T, HK, D)
+    out = varlen_attention(q.to(DEV), k.to(DEV), v.to(DEV), cu_seqlens_q=cu.to(DEV), cu_seqlens_k=cu.to(DEV),
+                           max_seqlen_q=max(lens), softmax_scale=SCALE, causal=True, quant=True)
+    _check(out, ref.varlen(q.float(), cu, cu, k=k, v=v), "per-XCD order int8")

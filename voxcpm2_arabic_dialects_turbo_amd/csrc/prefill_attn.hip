@@ -40,6 +40,8 @@ constexpr int kKsStride = kD + 16;
 constexpr int kVsStride = kD + 24;
 // word 3 of a raw buffer descriptor (32-bit data format; offsets in bytes, range-checked against num_records)
 constexpr int kBufferWord3 = 0x00020000;
+constexpr unsigned kXcds = 8;                  // MI355X: workgroups are dealt round-robin over 8 XCDs
+constexpr unsigned kXcdOrderMinWorkgroups = 1024;
 
 // Where a workgroup's keys come from (one kernel instance each, so no path's loop-carried state constrains another's
 // load waits): packed [Tk, HK, D] rows; the paged cache with block_size a multiple of 64 (a 64-key tile lies in one
@@ -53,10 +55,19 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
   __shared__ __attribute__((aligned(16))) uint16_t vs_all[NH][2][kBK][kVsStride];  // V double-buffered
   __shared__ unsigned s_amax[QUANT ? kRows : 1];  // QUANT: per token of the tile, float bits of max |o|
 
-  const int qt = blockIdx.x;
-  const int b = blockIdx.y;
+  // Work item (q tile, sequence, kv head). Workgroup i runs on XCD i % 8; with xcd_order each XCD gets a contiguous
+  // run of work items, so the query tiles that re-read a sequence's K/V tiles find them in that XCD's L2 (the
+  // launcher sets it for large grids; on small ones the runs would hold uneven numbers of empty tiles).
+  unsigned work = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  if (p.xcd_order) {
+    const unsigned nwg = gridDim.x * gridDim.y * gridDim.z;
+    const unsigned xq = nwg / kXcds, xr = nwg % kXcds, xcd = work % kXcds, loc = work / kXcds;
+    work = (xcd < xr ? xcd * (xq + 1) : xr * (xq + 1) + (xcd - xr) * xq) + loc;
+  }
+  const int qt = (int)(work % gridDim.x);
+  const int b = (int)((work / gridDim.x) % gridDim.y);
   const int half = QUANT ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8)) : 0;  // wave-uniform
-  const int g = QUANT ? half : (int)blockIdx.z;
+  const int g = QUANT ? half : (int)(work / (gridDim.x * gridDim.y));
   auto& ks = ks_all[half];
   auto& vs2 = vs_all[half];
   int q0, nq, k0, nk;
@@ -578,19 +589,23 @@ hipError_t launch_prefill_kind(const PrefillArgs& a, dim3 grid, dim3 block, hipS
   return hipGetLastError();
 }
 
-hipError_t launch_prefill(const PrefillArgs& a, int max_seqlen_q, hipStream_t stream) {
-  const int bq = kRows / a.group;
+hipError_t launch_prefill(const PrefillArgs& a0, int max_seqlen_q, hipStream_t stream) {
+  const int bq = kRows / a0.group;
   const int q_tiles = (max_seqlen_q + bq - 1) / bq;
-  if (q_tiles <= 0 || a.batch <= 0) return hipSuccess;
+  if (q_tiles <= 0 || a0.batch <= 0) return hipSuccess;
+  PrefillArgs a = a0;
+  a.xcd_order = (int64_t)q_tiles * a.batch * a.num_kv_heads >= kXcdOrderMinWorkgroups;
   return launch_prefill_kind<false>(a, dim3((unsigned)q_tiles, (unsigned)a.batch, (unsigned)a.num_kv_heads), dim3(256),
                                     stream);
 }
 
-hipError_t launch_prefill_int8(const PrefillArgs& a, int max_seqlen_q, hipStream_t stream) {
-  const int bq = kRows / a.group;
+hipError_t launch_prefill_int8(const PrefillArgs& a0, int max_seqlen_q, hipStream_t stream) {
+  const int bq = kRows / a0.group;
   const int q_tiles = (max_seqlen_q + bq - 1) / bq;
-  if (q_tiles <= 0 || a.batch <= 0) return hipSuccess;
-  if (a.num_kv_heads < 1 || a.num_kv_heads > 2) return hipErrorInvalidValue;
+  if (q_tiles <= 0 || a0.batch <= 0) return hipSuccess;
+  if (a0.num_kv_heads < 1 || a0.num_kv_heads > 2) return hipErrorInvalidValue;
+  PrefillArgs a = a0;
+  a.xcd_order = (int64_t)q_tiles * a.batch >= kXcdOrderMinWorkgroups;
   return launch_prefill_kind<true>(a, dim3((unsigned)q_tiles, (unsigned)a.batch, 1u), dim3(256 * a.num_kv_heads),
                                    stream);
 }

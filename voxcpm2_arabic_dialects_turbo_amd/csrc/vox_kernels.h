@@ -68,6 +68,7 @@ struct PrefillArgs {
   const float* inv_smooth;
   int8_t* out_q;              // int8 [T, H * 128]; token rows out_row_stride apart
   float* out_scale;           // fp32 [T]
+  int xcd_order;              // set by the launcher: run contiguous (q tile, sequence, kv head) ranges per XCD
 };
 
 struct CopyArgs {
