@@ -8,14 +8,18 @@
 // paged cache through block_tables, or from packed [Tk, HK, D] rows when there is no block table.
 //
 // gfx950 mapping. A workgroup (4 waves, 256 threads) owns 128 query rows = (128 / G tokens) x (the G query heads of
-// one kv head): GQA shares every K/V tile across the group's heads. Per 64-key tile the workgroup stages K and V
-// row-major in LDS (16-byte stores); each wave computes S^T[64 keys x 32 rows] = K Q^T with Q^T held in registers,
-// an online softmax in fp32 (exp2, log2-prescaled scale), and O^T[128 d x 32 rows] += V^T P^T, where P^T comes out of
-// the score MFMA already in B-operand layout and V^T is read with ds_read_b64_tr_b16 (two transposed reads give a
-// lane the 8 keys of one d column). The next tile's K/V loads are issued into registers before the current tile is
-// computed, so their latency hides behind the MFMA work; in paged mode the block ids are read one tile further
-// ahead, so a tile's loads never wait on a lookup. The causal / length mask is only evaluated on tiles that reach
-// past the first query's position or past the keys.
+// one kv head): GQA shares every K/V tile across the group's heads. Per 64-key tile K and V go from global memory
+// straight into LDS (range-checked buffer loads with the lds bit: no register staging; rows past the keys and
+// unmapped blocks read as zeros), double-buffered, with the 16-byte chunks of each 256-byte row permuted so that the
+// fragment reads meet no bank conflicts; each wave computes S^T[64 keys x 32 rows] = K Q^T with Q^T held in
+// registers, an online softmax in fp32 (exp2, log2-prescaled scale), and O^T[128 d x 32 rows] += V^T P^T, where P^T
+// comes out of the score MFMA already in B-operand layout and V^T is read with ds_read_b64_tr_b16 (two transposed
+// reads give a lane the 8 keys of one d column). The next tile's loads are issued before the current tile is
+// computed and waited for only at the tile's one barrier; in paged mode the block ids are read one tile further
+// ahead. The causal / length mask is only evaluated on tiles that reach past the first query's position or past
+// the keys. Large grids deal contiguous work ranges per XCD, so the query tiles that re-read a sequence's K/V find
+// it in that XCD's L2. (Paged caches whose block size is not a multiple of 64 stage per-piece loads through
+// registers instead.)
 //
 // int8 output (QUANT; reference: the QUANT epilogues of kernels/prefill_attn.py:84-92 and kernels/short_attn.py:
 // 55-64, 137-146): the o_proj GEMM takes o per token as int8 plus one fp32 scale over all heads, so a workgroup then
