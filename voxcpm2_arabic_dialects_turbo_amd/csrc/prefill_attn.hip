@@ -62,32 +62,40 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
   // Work item (q tile, sequence, kv head). Workgroup i runs on XCD i % 8; with xcd_order each XCD gets a contiguous
   // run of work items, so the query tiles that re-read a sequence's K/V tiles find them in that XCD's L2 (the
   // launcher sets it for large grids; on small ones the runs would hold uneven numbers of empty tiles).
-  unsigned work = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  int qt = blockIdx.x, b = blockIdx.y, gz = blockIdx.z;
   if (p.xcd_order) {
     const unsigned nwg = gridDim.x * gridDim.y * gridDim.z;
-    const unsigned xq = nwg / kXcds, xr = nwg % kXcds, xcd = work % kXcds, loc = work / kXcds;
-    work = (xcd < xr ? xcd * (xq + 1) : xr * (xq + 1) + (xcd - xr) * xq) + loc;
+    const unsigned id = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    const unsigned xq = nwg / kXcds, xr = nwg % kXcds, xcd = id % kXcds, loc = id / kXcds;
+    const unsigned work = (xcd < xr ? xcd * (xq + 1) : xr * (xq + 1) + (xcd - xr) * xq) + loc;
+    qt = (int)(work % gridDim.x);
+    b = (int)((work / gridDim.x) % gridDim.y);
+    gz = (int)(work / (gridDim.x * gridDim.y));
   }
-  const int qt = (int)(work % gridDim.x);
-  const int b = (int)((work / gridDim.x) % gridDim.y);
   const int half = QUANT ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8)) : 0;  // wave-uniform
-  const int g = QUANT ? half : (int)(work / (gridDim.x * gridDim.y));
+  const int g = QUANT ? half : gz;
   auto& ks = ks_all[half];
   auto& vs2 = vs_all[half];
+  // the sequence bounds, and the first key tile's block id (table column 0) beside them rather than after them
   int q0, nq, k0, nk;
-  if (p.cu_q) {
-    q0 = p.cu_q[b];
-    nq = p.cu_q[b + 1] - q0;
-  } else {
+  int bid0 = 0;
+  {
+    int q1, k1;
     q0 = b * p.uniform_q;
-    nq = p.uniform_q;
-  }
-  if (p.cu_k) {
-    k0 = p.cu_k[b];
-    nk = p.cu_k[b + 1] - k0;
-  } else {
+    q1 = q0 + p.uniform_q;
     k0 = b * p.uniform_k;
-    nk = p.uniform_k;
+    k1 = k0 + p.uniform_k;
+    if (p.cu_q) {
+      q0 = p.cu_q[b];
+      q1 = p.cu_q[b + 1];
+    }
+    if (p.cu_k) {
+      k0 = p.cu_k[b];
+      k1 = p.cu_k[b + 1];
+    }
+    if constexpr (KV == kPagedTiles) bid0 = p.block_tables[(int64_t)b * p.bt_stride];
+    nq = q1 - q0;
+    nk = k1 - k0;
   }
   if (KV != kPacked) nk = min(nk, p.max_blocks * p.block_size);  // keys the block table can address
   const int G = p.group;
@@ -475,7 +483,7 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
       __syncthreads();  // the next tile has landed (the barrier waits for this wave's DMA) and this one is free
     };
     if (kv_end > 0) {
-      fetch_bids(0);
+      tile_bid = bid0;
       dma(kt0[half], vt0[half], 0);
       fetch_bids(kBK);
       wait_vmem_all();  // the query and tile 0
