@@ -292,3 +292,15 @@ def test_large_ragged_grid_in_per_xcd_order():
                                   _cu(lens).to(DEV), softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
     wantp = ref.varlen(qp.float(), _cu(nq), _cu(lens), k_cache=kc, v_cache=vc, block_tables=tables)
     attn_close(outp, wantp, "per-XCD order, paged")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_uniform_lengths_over_several_key_tiles(causal):
+    """The uniform-length mode (no cu_seqlens: flash_attn_func) over several 64-key tiles with a ragged last one:
+    3 sequences of 300 queries over 333 keys, non-causal and bottom-right causal."""
+    gen = torch.Generator().manual_seed(76 + causal)
+    B, L, Lk = 3, 300, 333
+    q, k, v = randn(gen, B, L, H, D), randn(gen, B, Lk, HK, D), randn(gen, B, Lk, HK, D)
+    out = flash_attn_func(q.to(DEV), k.to(DEV), v.to(DEV), softmax_scale=SCALE, causal=causal)
+    want = ref.dense(q.float(), k.float(), v.float(), causal=causal)
+    attn_close(out, want, f"uniform lengths, causal={causal}")
