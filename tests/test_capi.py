@@ -80,7 +80,7 @@ def test_decode_workspace_and_grid_choice():
     def need(b, g):
         up = lambda x: -(-x // 256) * 256
         s = min(b, 512)  # sequences per launch
-        return up((s + g) * (16 * 128 + 32) * 4) + up((s + 1) * 4)
+        return up((s + g) * (16 * 128 + 32) * 4) + up((s + 2) * 4)
     for b in (1, 40, 150, 512, 5000):
         assert lib.vox_decode_workspace_bytes(b) == need(b, grid)
     lib.vox_set_decode_workgroups(7)

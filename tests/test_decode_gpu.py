@@ -88,7 +88,7 @@ def test_decode_strided_query_rows_and_small_blocks():
 @pytest.mark.parametrize("grid", [1, 2, 7, 64, 333, 768, 4000])
 def test_decode_split_grids_agree(grid):
     """The split kernel's range partition at many grid sizes: one workgroup holding every sequence, ranges cutting
-    sequences anywhere, more workgroups than steps (empty ranges)."""
+    sequences anywhere, more workgroups than steps (the launch then uses one per step)."""
     gen = torch.Generator().manual_seed(35)
     lens = uniform_lens(gen, 20, 1, 2048) + [0, 64, 65]
     kc, vc, tables = paged_pool(gen, [max(n, 1) for n in lens], 200)
@@ -99,6 +99,21 @@ def test_decode_split_grids_agree(grid):
         assert int(out[20].abs().sum()) == 0
     finally:
         lib.vox_set_decode_workgroups(0)
+
+
+@pytest.mark.parametrize("lens", [[16384], [4096] * 4, [300] * 16 + [8192], [5, 9000, 3, 0, 2100, 64]],
+                         ids=["1x16384", "4x4096", "16x300+8192", "mixed"])
+def test_decode_few_long_sequences(lens):
+    """Few sequences, some far longer than a workgroup's share of the steps: the launch then uses fewer workgroups
+    (no sequence is cut into more than about 32 partials) and the merge kernel folds the partials of one sequence in
+    several batches of loads."""
+    gen = torch.Generator().manual_seed(40)
+    pool = sum((max(n, 1) + BLOCK - 1) // BLOCK for n in lens) + 4
+    kc, vc, tables = paged_pool(gen, [max(n, 1) for n in lens], pool)
+    (_, _), out = _check(randn(gen, len(lens), H, D), kc, vc, lens, tables, f"lens {lens[:6]}")
+    for i, n in enumerate(lens):
+        if n == 0:
+            assert int(out[i].abs().sum()) == 0
 
 
 def test_decode_repeated_calls_of_changing_batch():

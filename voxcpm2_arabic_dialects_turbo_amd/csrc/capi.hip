@@ -78,7 +78,7 @@ void vox_set_decode_workgroups(int workgroups) { g_decode_grid_override = workgr
 
 namespace {
 // Workspace of one decode launch of `slice` sequences: fp32 partials [slice + grid] then the int32 step layout
-// [slice + 1], each 256-byte aligned.
+// [slice + 2] (first step of every sequence, the total, the active workgroup count), each 256-byte aligned.
 size_t decode_partials_bytes(int slice, int grid) {
   return ((size_t)(slice + grid) * vox::kPartialFloats * sizeof(float) + 255) / 256 * 256;
 }
@@ -87,7 +87,7 @@ size_t decode_partials_bytes(int slice, int grid) {
 size_t vox_decode_workspace_bytes(int batch) {
   if (batch <= 0) return 0;
   const int slice = batch < vox::kMaxSeqPerLaunch ? batch : vox::kMaxSeqPerLaunch;
-  return decode_partials_bytes(slice, vox_decode_workgroups()) + ((size_t)(slice + 1) * 4 + 255) / 256 * 256;
+  return decode_partials_bytes(slice, vox_decode_workgroups()) + ((size_t)(slice + 2) * 4 + 255) / 256 * 256;
 }
 
 int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,

@@ -39,6 +39,17 @@ constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * kWave;
 constexpr int kStep = kWaves * kTile;  // tokens per workgroup step
 constexpr int kMaxHeads = 16;
+#ifndef VOX_MAX_PIECES
+#define VOX_MAX_PIECES 32
+#endif
+#ifndef VOX_MERGE_BATCH
+#define VOX_MERGE_BATCH 8
+#endif
+// Most partials one sequence is cut into. A sequence of n steps meets at most about n G / S + 2 of G equal ranges of
+// S steps, so a launch uses G' = min(grid, (kMaxPieces - 2) S / n_max) workgroups (the others leave after the layout
+// scan): a long sequence among few is not cut into one-step pieces, each a partial for the merge kernel to load.
+constexpr int kMaxPieces = VOX_MAX_PIECES;
+constexpr int kMergeBatch = VOX_MERGE_BATCH;  // partials whose loads the merge kernel keeps in flight together
 
 __device__ __forceinline__ f32x4 mfma_16x16x16(s16x4 a, s16x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
@@ -81,6 +92,13 @@ __device__ __forceinline__ int64_t muldiv(int64_t a, int64_t b, int64_t c, int64
   return (int64_t)(num / (uint64_t)d);
 }
 
+// G' of a launch over `steps` steps whose longest sequence has `max_seq_steps`; at most `steps`, so no range is empty
+__device__ __forceinline__ int active_workgroups(int grid, int64_t steps, int max_seq_steps) {
+  if (max_seq_steps <= 0) return 1;
+  const int64_t cap = min(steps, muldiv(kMaxPieces - 2, steps, 0, max_seq_steps));
+  return (int)max((int64_t)1, min((int64_t)grid, cap));
+}
+
 // A value every lane of the wave holds, moved to a scalar register (LDS reads land in vector registers).
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
@@ -106,10 +124,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   __shared__ int s_ctx[kMaxSeqPerLaunch];        // context per sequence, cut to the table's reach
   __shared__ int s_start[kMaxSeqPerLaunch + 1];  // first step per sequence; s_start[batch] = total steps
   __shared__ int s_wtot[kWaves];
+  __shared__ int s_wmax[kWaves];  // most steps of one sequence, per wave
   __shared__ int s_bt[kBtLds];  // the block table, when it fits: no block-id round trips at segment starts
 
   const int g = blockIdx.x;
-  const int G = gridDim.x;
   const int tid = threadIdx.x;
   const int w = tid >> 6;
   const int lane = tid & 63;
@@ -123,18 +141,26 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   if constexpr (BTL)
     for (int i = tid; i < p.batch * mb; i += kThreads) s_bt[i] = p.block_tables[(int64_t)(i / mb) * p.bt_stride + i % mb];
   int run = 0;
+  int nmax = 0;  // most steps of one sequence
   for (int base = 0; base < p.batch; base += kThreads) {
     const int bb = base + tid;
     const int ctx = bb < p.batch ? max(0, min(p.context_lens[bb], max_ctx)) : 0;
     const int n = (ctx + kStep - 1) / kStep;
     const int incl = wave_incl_scan(n, lane);
-    if (lane == kWave - 1) s_wtot[w] = incl;
+    int wmax = n;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) wmax = max(wmax, __shfl_xor(wmax, o, kWave));
+    if (lane == kWave - 1) {
+      s_wtot[w] = incl;
+      s_wmax[w] = wmax;
+    }
     __syncthreads();
     int before = 0, total = 0;
 #pragma unroll
     for (int ww = 0; ww < kWaves; ++ww) {
       before += ww < w ? s_wtot[ww] : 0;
       total += s_wtot[ww];
+      nmax = max(nmax, s_wmax[ww]);
     }
     if (bb < p.batch) {
       s_ctx[bb] = ctx;
@@ -146,11 +172,15 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   if (tid == 0) s_start[p.batch] = run;
   __syncthreads();
   const int S = uniform(run);
-  if (g == 0)  // the layout decode_merge_kernel reads
+  const int G = active_workgroups(gridDim.x, S, uniform(nmax));
+  if (g == 0) {  // the layout decode_merge_kernel reads, then the active workgroup count
     for (int i = tid; i <= p.batch; i += kThreads) p.steps[i] = s_start[i];
+    if (tid == 0) p.steps[p.batch + 1] = G;
+  }
 
   // this workgroup's range [r, r1) and the sequence holding its first step: the last b with s_start[b] <= r
   // (an empty sequence shares its start with the next one, so the last such b is not empty)
+  if (g >= G) return;  // workgroup-uniform; WG 0 (always active) published the layout
   const int r1 = (int)muldiv(g + 1, S, 0, G);
   int r = (int)muldiv(g, S, 0, G);
   int b = 0;
@@ -190,28 +220,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
       else return bt_row[col];
     };
 
-    // The query row and the block id of this wave's first tile load together. Query row of head r16:
-    // d = kq*32 + jq*8 + [0, 8); the score B operand for k-step kc is piece kc % 4 when kc's kv head (kc / 4) is
-    // the lane's group, else zero: block-diagonal over (kv head, d).
-    u32x4 qv[4];
-    {
-      const uint16_t* qb = p.q + (int64_t)b * p.q_row_stride + (int64_t)(h < H ? h : 0) * kD + jq * 8;
-#pragma unroll
-      for (int kq = 0; kq < 4; ++kq) qv[kq] = ld_g16(qb + kq * 32);
-    }
-
-    // the score MFMA's B operands for the segment: block-diagonal over (kv head, d)
-    u32x4 qop[TT::KC];
-#pragma unroll
-    for (int kc = 0; kc < TT::KC; ++kc) qop[kc] = hg == kc / 4 ? qv[kc % 4] : zero4();
-    const float c = p.scale_log2;
-
-    float m = -INFINITY;
-    float lsum = 0.f;
-    f32x4 acc[8];
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
     // per-lane byte offsets of the tile loads: K row r16, dims jq*8 + [0, 8) (+ 32 per k-step); V piece 0 = row
     // lane / PPR, dims (lane % PPR) * 8 + [0, 8)
     const uint32_t koff = (uint32_t)(r16 * TT::ROW + jq * 8) * 2u;
@@ -221,87 +229,111 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
       T.ok = blk >= 0 && blk < p.num_blocks;
       load_tile<HK>(T, p, (T.ok ? blk : 0) * p.block_size + (t0 % p.block_size), koff, voff);
     };
-    // Scores, online softmax and P V of one loaded tile. The scale goes into the exp2 argument (one FMA); the running
-    // max moves (rescaling acc and lsum) only when the tile max exceeds it by more than 8 in log2 units (p <= 256,
-    // exact after the final 1 / l); the masks and zero selects run only on a tile that is not fully valid.
-    auto compute = [&](const Tile<HK>& T, int t0) {
-      f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kc = 0; kc < TT::KC; ++kc) s = mfma_16x16x32(T.k[kc], qop[kc], s);
-      const bool full = T.ok && t0 + kTile <= tok_end;  // wave-uniform
-      // lane (head r16) holds tokens t0 + jq*4 + [0, 4)
-      float x[4];
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        x[rr] = full || (T.ok && (t0 + jq * 4 + rr) < tok_end) ? s[rr] : -INFINITY;
-      const float tm = col_max4(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]))) * c;
-      const bool up = tm > m + 8.f;
-      if (__builtin_amdgcn_ballot_w64(up) != 0) {  // wave-uniform
-        const float alpha = up ? fast_exp2(m - tm) : 1.f;  // exp2(-inf) = 0 on the first update
-        m = up ? tm : m;
-        lsum *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
-      }
-      const float mu = m == -INFINITY ? 0.f : m;
-      float ps = 0.f;
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        x[rr] = fast_exp2(fmaf(x[rr], c, -mu));
-        ps += x[rr];
-      }
-      lsum += ps;
 
-      // V tile -> LDS, row-major, 16-byte stores; rows of tokens past tok_end or of an unmapped block are zeroed
-      // (they meet p = 0 in P V, and unwritten cache slots may hold any bit pattern)
-      if (full) {
+    float m = -INFINITY;
+    float lsum = 0.f;
+    f32x4 acc[8];
 #pragma unroll
-        for (int i = 0; i < TT::VP; ++i) {
-          const int pc = i * 64 + lane;
-          *reinterpret_cast<u32x4*>(vt + (pc / TT::PPR) * VROW + (pc % TT::PPR) * 8) = T.v[i];
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < TT::VP; ++i) {
-          const int pc = i * 64 + lane;
-          const bool ok = T.ok && (t0 + pc / TT::PPR) < tok_end;
-          *reinterpret_cast<u32x4*>(vt + (pc / TT::PPR) * VROW + (pc % TT::PPR) * 8) = ok ? T.v[i] : zero4();
-        }
-      }
-      wave_lds_sync();
+    for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-      // P^T operand: k-slots jq*4 + [0, 4) = tokens jq*4 + [0, 4)
-      const uint32_t p01 = pack_bf16x2(x[0], x[1]);
-      const uint32_t p23 = pack_bf16x2(x[2], x[3]);
-      const s16x4 pv = __builtin_bit_cast(s16x4, u32x2{p01, p23});
-      const s16x4 pz = s16x4{0, 0, 0, 0};
-#pragma unroll
-      for (int gk = 0; gk < HK; ++gk) {
-        const s16x4 pb = (hg == gk) ? pv : pz;
-#pragma unroll
-        for (int d4 = 0; d4 < 8; d4 += 4) {
-          s16x4 va[4];
-#pragma unroll
-          for (int u = 0; u < 4; ++u) va[u] = lds_read_tr16(vtr + gk * kD + (d4 + u) * 16);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) acc[d4 + u] = mfma_16x16x16(va[u], pb, acc[d4 + u]);
-        }
-      }
-      wave_lds_sync();
-    };
-
-    // This wave's tiles: first, first + kStep, ...; the block id of the next tile is read with the current tile's
-    // loads, so the loop never waits on a lookup alone.
+    // This wave's tiles: first, first + kStep, ... (a wave with none adds m = -inf, l = 0 to the merge). The query
+    // row and the first tile load together, the query first, so that building the score operands waits for it alone
+    // (all of this sits inside the branch: where a path without the tile loads joins, the compiler's wait counts
+    // would also cover the tile); the block id of the second tile is read meanwhile. Each later tile's loads go out
+    // as soon as the previous tile is computed, with the block id of the tile after it. Query row of head r16:
+    // d = kq*32 + jq*8 + [0, 8); the score B operand for k-step kc is piece kc % 4 when kc's kv head (kc / 4) is
+    // the lane's group, else zero: block-diagonal over (kv head, d).
     const int first = tok0 + w * kTile;
     if (first < tok_end) {
-      int64_t blk = block_of(first / p.block_size);
+      u32x4 qv[4];
+      {
+        const uint16_t* qb = p.q + (int64_t)b * p.q_row_stride + (int64_t)(h < H ? h : 0) * kD + jq * 8;
+#pragma unroll
+        for (int kq = 0; kq < 4; ++kq) qv[kq] = ld_g16(qb + kq * 32);
+      }
+      Tile<HK> T;
+      issue(T, block_of(first / p.block_size), first);
+      int64_t blk_next = block_of(min(first + kStep, tok_end - 1) / p.block_size);
+      u32x4 qop[TT::KC];
+#pragma unroll
+      for (int kc = 0; kc < TT::KC; ++kc) qop[kc] = hg == kc / 4 ? qv[kc % 4] : zero4();
+      const float c = p.scale_log2;
+
+      // Scores, online softmax and P V of one loaded tile. The scale goes into the exp2 argument (one FMA); the running
+      // max moves (rescaling acc and lsum) only when the tile max exceeds it by more than 8 in log2 units (p <= 256,
+      // exact after the final 1 / l); the masks and zero selects run only on a tile that is not fully valid.
+      auto compute = [&](const Tile<HK>& T, int t0) {
+        f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < TT::KC; ++kc) s = mfma_16x16x32(T.k[kc], qop[kc], s);
+        const bool full = T.ok && t0 + kTile <= tok_end;  // wave-uniform
+        // lane (head r16) holds tokens t0 + jq*4 + [0, 4)
+        float x[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          x[rr] = full || (T.ok && (t0 + jq * 4 + rr) < tok_end) ? s[rr] : -INFINITY;
+        const float tm = col_max4(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]))) * c;
+        const bool up = tm > m + 8.f;
+        if (__builtin_amdgcn_ballot_w64(up) != 0) {  // wave-uniform
+          const float alpha = up ? fast_exp2(m - tm) : 1.f;  // exp2(-inf) = 0 on the first update
+          m = up ? tm : m;
+          lsum *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+        }
+        const float mu = m == -INFINITY ? 0.f : m;
+        float ps = 0.f;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          x[rr] = fast_exp2(fmaf(x[rr], c, -mu));
+          ps += x[rr];
+        }
+        lsum += ps;
+
+        // V tile -> LDS, row-major, 16-byte stores; rows of tokens past tok_end or of an unmapped block are zeroed
+        // (they meet p = 0 in P V, and unwritten cache slots may hold any bit pattern)
+        if (full) {
+#pragma unroll
+          for (int i = 0; i < TT::VP; ++i) {
+            const int pc = i * 64 + lane;
+            *reinterpret_cast<u32x4*>(vt + (pc / TT::PPR) * VROW + (pc % TT::PPR) * 8) = T.v[i];
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < TT::VP; ++i) {
+            const int pc = i * 64 + lane;
+            const bool ok = T.ok && (t0 + pc / TT::PPR) < tok_end;
+            *reinterpret_cast<u32x4*>(vt + (pc / TT::PPR) * VROW + (pc % TT::PPR) * 8) = ok ? T.v[i] : zero4();
+          }
+        }
+        wave_lds_sync();
+
+        // P^T operand: k-slots jq*4 + [0, 4) = tokens jq*4 + [0, 4)
+        const uint32_t p01 = pack_bf16x2(x[0], x[1]);
+        const uint32_t p23 = pack_bf16x2(x[2], x[3]);
+        const s16x4 pv = __builtin_bit_cast(s16x4, u32x2{p01, p23});
+        const s16x4 pz = s16x4{0, 0, 0, 0};
+#pragma unroll
+        for (int gk = 0; gk < HK; ++gk) {
+          const s16x4 pb = (hg == gk) ? pv : pz;
+#pragma unroll
+          for (int d4 = 0; d4 < 8; d4 += 4) {
+            s16x4 va[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) va[u] = lds_read_tr16(vtr + gk * kD + (d4 + u) * 16);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[d4 + u] = mfma_16x16x16(va[u], pb, acc[d4 + u]);
+          }
+        }
+        wave_lds_sync();
+      };
+
       for (int t0 = first; t0 < tok_end; t0 += kStep) {
-        const int64_t blk_next = block_of(min(t0 + kStep, tok_end - 1) / p.block_size);
-        Tile<HK> T;
-        issue(T, blk, t0);
-        __builtin_amdgcn_sched_barrier(0);  // all of the tile's loads issue before any of them is waited on
         compute(T, t0);
-        blk = blk_next;
+        if (t0 + kStep < tok_end) {
+          issue(T, blk_next, t0 + kStep);
+          blk_next = block_of(min(t0 + 2 * kStep, tok_end - 1) / p.block_size);
+        }
       }
     }
 
@@ -363,10 +395,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
 
 // Writes the sequences that decode_kernel left as partials, and the zeros of empty rows. One workgroup per
 // sequence, thread = (head, 8 dims). Sequence b covers steps [sb, eb) of the layout decode_kernel published in
-// `steps`; workgroup g of G covers
-// [floor(g S / G), floor((g + 1) S / G)); the workgroups touching b are g_first..g_last below, each left a partial at
-// slot b + g unless its range is empty. Online rescale over the partials (fp32), partial loads of four workgroups
-// in flight together. Runs after decode_kernel on the same stream, which makes the partials visible.
+// `steps`, with the number G of workgroups it used; workgroup g of G covers [floor(g S / G), floor((g + 1) S / G))
+// (at least one step, as G <= S), and the workgroups touching b, g_first..g_last below, each left a partial at slot
+// b + g. Online rescale over the partials (fp32), the loads of kMergeBatch partials in flight together. Runs after
+// decode_kernel on the same stream, which makes the partials visible.
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs p) {
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
@@ -376,13 +408,13 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs p) {
   const int64_t S = p.steps[p.batch];
   const int64_t sb = p.steps[b];
   const int64_t eb = p.steps[b + 1];
+  const int64_t G = p.steps[p.batch + 1];  // active workgroups (with S >= 1, none has an empty range)
   uint16_t* ob = p.out + ((int64_t)b * H + hh) * kD + d0;
   if (hh >= H) return;
   if (eb == sb) {  // empty (padded) row: defined zeros
     *reinterpret_cast<u32x4*>(ob) = zero4();
     return;
   }
-  const int64_t G = p.grid;
   const int g_first = (int)muldiv(sb + 1, G, S - 1, S) - 1;
   const int g_last = (int)min(G - 1, muldiv(eb, G, S - 1, S) - 1);
   if (g_first >= g_last) return;  // one workgroup held the whole sequence and wrote it
@@ -391,21 +423,27 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs p) {
   float o2[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) o2[i] = 0.f;
-  for (int g0 = g_first; g0 <= g_last; g0 += 4) {
-    float mc[4], lc[4];
-    f32x4 oa[4], obv[4];
+  for (int g0 = g_first; g0 <= g_last; g0 += kMergeBatch) {
+    float mc[kMergeBatch], lc[kMergeBatch];
+    f32x4 oa[kMergeBatch], obv[kMergeBatch];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int64_t gg = min(g0 + u, g_last);
-      const bool live = g0 + u <= g_last && muldiv(gg, S, 0, G) < muldiv(gg + 1, S, 0, G);  // empty: wrote nothing
-      const float* pc = p.partials + (b + gg) * kPartialFloats;
-      mc[u] = live ? pc[kMaxHeads * kD + hh] : -INFINITY;
-      lc[u] = live ? pc[kMaxHeads * kD + kMaxHeads + hh] : 0.f;
-      oa[u] = live ? *reinterpret_cast<const f32x4*>(&pc[hh * kD + d0]) : f32x4{0.f, 0.f, 0.f, 0.f};
-      obv[u] = live ? *reinterpret_cast<const f32x4*>(&pc[hh * kD + d0 + 4]) : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < kMergeBatch; ++u) {
+      mc[u] = -INFINITY;
+      lc[u] = 0.f;
+      oa[u] = obv[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      // loads only up to the sequence's last range: the condition is workgroup-uniform, so the slots past it
+      // cost no traffic
+      const int64_t gg = g0 + u;
+      if (gg <= g_last) {
+        const float* pc = p.partials + (b + gg) * kPartialFloats;
+        mc[u] = pc[kMaxHeads * kD + hh];
+        lc[u] = pc[kMaxHeads * kD + kMaxHeads + hh];
+        oa[u] = *reinterpret_cast<const f32x4*>(&pc[hh * kD + d0]);
+        obv[u] = *reinterpret_cast<const f32x4*>(&pc[hh * kD + d0 + 4]);
+      }
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kMergeBatch; ++u) {
       const float mn = fmaxf(M2, mc[u]);
       const float mu = mn == -INFINITY ? 0.f : mn;
       const float a = fast_exp2(M2 - mu);

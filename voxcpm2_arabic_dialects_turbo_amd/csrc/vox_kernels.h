@@ -30,7 +30,7 @@ struct DecodeArgs {
   float scale_log2;           // softmax_scale * log2(e)
   int grid;                   // workgroups of the split kernel (persistent, balanced ranges)
   float* partials;            // [B + grid, kPartialFloats]
-  int32_t* steps;             // [B + 1]: first 64-token step of every sequence, then the total
+  int32_t* steps;             // [B + 2]: first 64-token step of every sequence, the total, the active workgroups
   uint16_t* out;              // bf16 [B, H, 128], contiguous
 };
 
