@@ -304,3 +304,26 @@ def test_uniform_lengths_over_several_key_tiles(causal):
     out = flash_attn_func(q.to(DEV), k.to(DEV), v.to(DEV), softmax_scale=SCALE, causal=causal)
     want = ref.dense(q.float(), k.float(), v.float(), causal=causal)
     attn_close(out, want, f"uniform lengths, causal={causal}")
+
+
+@pytest.mark.parametrize("bs", [None, 256, 48])
+def test_grid_above_the_eight_wave_limit(bs):
+    """A grid of more than 2048 workgroups (128 q tiles x 12 sequences x 2 kv heads), which the launcher runs with
+    4-wave workgroups of 32 rows each (smaller grids take 8 waves of 16 rows): one 2048-token causal sequence among
+    short ones, packed keys and paged caches (block size 256: one block id per key tile; 48: per-piece block ids)."""
+    gen = torch.Generator().manual_seed(81 + (bs or 0))
+    lens = [2048, 50, 7, 300, 1, 129, 64, 77, 1000, 3, 250, 16]
+    T = sum(lens)
+    q = randn(gen, T, H, D)
+    if bs is None:
+        k, v = randn(gen, T, HK, D), randn(gen, T, HK, D)
+        out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), max(lens), _cu(lens).to(DEV), max(lens),
+                                     _cu(lens).to(DEV), softmax_scale=SCALE, causal=True)
+        want = ref.varlen(q.float(), _cu(lens), _cu(lens), k=k, v=v)
+    else:
+        kc, vc, tables = paged_pool(gen, lens, sum((n + bs - 1) // bs for n in lens) + 2, block_size=bs)
+        out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), max(lens), _cu(lens).to(DEV), max(lens),
+                                     _cu(lens).to(DEV), softmax_scale=SCALE, causal=True,
+                                     block_table=tables.to(DEV))
+        want = ref.varlen(q.float(), _cu(lens), _cu(lens), k_cache=kc, v_cache=vc, block_tables=tables)
+    attn_close(out, want, f"4-wave grid, block_size {bs}")

@@ -7,12 +7,12 @@
 // j <= nk - nq + i (bottom-right aligned), o = softmax(scale * q k^T) v in fp32, stored as bf16. Keys come from the
 // paged cache through block_tables, or from packed [Tk, HK, D] rows when there is no block table.
 //
-// gfx950 mapping. A workgroup (4 waves, 256 threads) owns 128 query rows = (128 / G tokens) x (the G query heads of
-// one kv head): GQA shares every K/V tile across the group's heads. Per 64-key tile K and V go from global memory
-// straight into LDS (range-checked buffer loads with the lds bit: no register staging; rows past the keys and
-// unmapped blocks read as zeros), double-buffered, with the 16-byte chunks of each 256-byte row permuted so that the
-// fragment reads meet no bank conflicts; each wave computes S^T[64 keys x 32 rows] = K Q^T with Q^T held in
-// registers, an online softmax in fp32 (exp2, log2-prescaled scale), and O^T[128 d x 32 rows] += V^T P^T, where P^T
+// gfx950 mapping. A workgroup (4 waves of 32 rows on grids above 2048 workgroups, else 8 waves of 16) owns 128 query
+// rows = (128 / G tokens) x (the G query heads of one kv head): GQA shares every K/V tile across the group's heads.
+// Per 64-key tile K and V go from global memory straight into LDS (range-checked buffer loads with the lds bit: no
+// register staging; rows past the keys and unmapped blocks read as zeros), double-buffered, with the 16-byte chunks
+// of each 256-byte row permuted so that the fragment reads meet no bank conflicts; each wave computes S^T[64 keys x its rows] = K Q^T with Q^T held in
+// registers, an online softmax in fp32 (exp2, log2-prescaled scale), and O^T[128 d x rows] += V^T P^T, where P^T
 // comes out of the score MFMA already in B-operand layout and V^T is read with ds_read_b64_tr_b16 (two transposed
 // reads give a lane the 8 keys of one d column). The next tile's loads are issued before the current tile is
 // computed and waited for only at the tile's one barrier; in paged mode the block ids are read one tile further
@@ -46,15 +46,26 @@ constexpr int kVsStride = kD + 24;
 constexpr int kBufferWord3 = 0x00020000;
 constexpr unsigned kXcds = 8;                  // MI355X: workgroups are dealt round-robin over 8 XCDs
 constexpr unsigned kXcdOrderMinWorkgroups = 1024;
+// Grids of up to this many workgroups take 8-wave workgroups (measured, bf16 output, causal: 1 x 512 tokens 14.5 ->
+// 12.2 us, 44 x 46 paged over a 50-token prefix -4 %, 16 x 512 -3 %, 4 x 2048 -4 %, 2 x 8192 -3 %; at 4096
+// workgroups (16 x 2048, 64 x 512) the 4-wave form is 2-3 % faster).
+constexpr int64_t kSmallGridWorkgroups = 2048;
 
 // Where a workgroup's keys come from (one kernel instance each, so no path's loop-carried state constrains another's
 // load waits): packed [Tk, HK, D] rows; the paged cache with block_size a multiple of 64 (a 64-key tile lies in one
 // block: one block id per tile); the paged cache with any other block size (one block id per 16-byte piece).
 enum KvSource { kPacked = 0, kPagedTiles = 1, kPagedPieces = 2 };
 
-template <bool QUANT, int KV>
-__global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kernel(PrefillArgs p) {
+// NW waves per KV group, each owning RT 16-row blocks of the 128 query rows: 4 waves x 32 rows keep the LDS reads per
+// MFMA low (the largest grids); 8 waves x 16 rows halve each wave's work per key tile, which shortens a workgroup's
+// chain of key tiles (smaller grids, where the longest chains end the launch).
+template <bool QUANT, int KV, int NW>
+__global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 : 2) void prefill_kernel(PrefillArgs p) {
   constexpr int NH = QUANT ? 2 : 1;  // KV-group halves per workgroup
+  constexpr int RT = 8 / NW;         // 16-row blocks per wave
+  constexpr int NT = 64 * NW;        // threads per KV group
+  constexpr int PR = 4 * NW;         // tile rows one load instruction of the group covers (16 bytes per thread)
+  constexpr int NP = kBK / PR;       // load instructions per thread per 64-key tile
   __shared__ __attribute__((aligned(16))) uint16_t ks_all[NH][kBK][kKsStride];
   __shared__ __attribute__((aligned(16))) uint16_t vs_all[NH][2][kBK][kVsStride];  // V double-buffered
   __shared__ unsigned s_amax[QUANT ? kRows : 1];  // QUANT: per token of the tile, float bits of max |o|
@@ -75,7 +86,7 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
     gz = (int)(work / (gridDim.x * gridDim.y));
     if (p.causal) qt = (int)gridDim.x - 1 - qt;  // heavy query tiles first
   }
-  const int half = QUANT ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8)) : 0;  // wave-uniform
+  const int half = QUANT ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x / NT)) : 0;  // wave-uniform
   const int g = QUANT ? half : gz;
   auto& ks = ks_all[half];
   auto& vs2 = vs_all[half];
@@ -105,7 +116,7 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
   const int BQ = kRows / G;  // query tokens per workgroup
   if (qt * BQ >= nq) return;
 
-  const int tid = threadIdx.x & 255;  // thread within the half
+  const int tid = threadIdx.x & (NT - 1);  // thread within the half
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   if constexpr (QUANT)
     if (threadIdx.x < (unsigned)BQ) s_amax[threadIdx.x] = 0u;  // ordered before the atomics by the barriers below
@@ -114,15 +125,15 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
   const int jq = lane >> 4;
   const int HK = p.num_kv_heads;
 
-  // This lane's two query rows (one per 16-row MFMA column tile): rho = w*32 + rt*16 + r16.
-  u32x4 qop[2][4];
-  bool row_ok[2];
-  int qpos[2];
-  int tq_of[2];
-  int h_of[2];
+  // This lane's RT query rows (one per 16-row MFMA column tile): rho = w*16*RT + rt*16 + r16.
+  u32x4 qop[RT][4];
+  bool row_ok[RT];
+  int qpos[RT];
+  int tq_of[RT];
+  int h_of[RT];
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    const int rho = w * 32 + rt * 16 + r16;
+  for (int rt = 0; rt < RT; ++rt) {
+    const int rho = (w * RT + rt) * 16 + r16;
     const int tq = qt * BQ + rho / G;
     const int h = g * G + rho % G;
     tq_of[rt] = tq;
@@ -137,15 +148,19 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
   const int tq_last = min(nq, (qt + 1) * BQ) - 1;
   const int kv_end = p.causal ? min(nk, nk - nq + tq_last + 1) : nk;
 
-  float m[2] = {-INFINITY, -INFINITY};
-  float l[2] = {0.f, 0.f};
-  f32x4 acc[8][2];
+  float m[RT], l[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    m[rt] = -INFINITY;
+    l[rt] = 0.f;
+  }
+  f32x4 acc[8][RT];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) acc[dt][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int rt = 0; rt < RT; ++rt) acc[dt][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // ---- K/V tile pieces: piece i of a tile is key lrow + 16 i, dims dc .. dc + 8 (16 bytes per thread). Packed keys
+  // ---- K/V tile pieces: piece i of a tile is key lrow + PR i, dims dc .. dc + 8 (16 bytes per thread). Packed keys
   // and paged tiles inside one cache block (block_size a multiple of 64) go straight to LDS (the DMA path below);
   // other block sizes read each piece's block id one tile ahead (fetch_bids) and stage through registers.
   constexpr bool paged = KV != kPacked;
@@ -154,8 +169,10 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
   const int rs_v = paged ? HK * kD : (int)p.v_row_stride;
   const int lrow = tid >> 4;
   const int dc = (tid & 15) * 8;
-  u32x4 kr[4], vr[4];
-  int bids[4] = {0, 0, 0, 0};  // per-piece block ids (paged, block_size not a multiple of 64)
+  u32x4 kr[NP], vr[NP];
+  int bids[NP];  // per-piece block ids (paged, block_size not a multiple of 64)
+#pragma unroll
+  for (int i = 0; i < NP; ++i) bids[i] = 0;
   int tile_bid = 0;            // the block id of the next tile to load (paged, block_size a multiple of 64)
   unsigned live = 0;           // bit i: piece i is a real key
   auto fetch_bids = [&](int kv0) {
@@ -165,8 +182,8 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
       return;
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int jc = min(kv0 + lrow + 16 * i, nk - 1);
+    for (int i = 0; i < NP; ++i) {
+      const int jc = min(kv0 + lrow + PR * i, nk - 1);
       bids[i] = p.block_tables[(int64_t)b * p.bt_stride + jc / p.block_size];
     }
   };
@@ -175,8 +192,8 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
   auto load_tile = [&](int kv0) {
     live = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int jj = kv0 + lrow + 16 * i;
+    for (int i = 0; i < NP; ++i) {
+      const int jj = kv0 + lrow + PR * i;
       const int jc = min(jj, nk - 1);
       const int64_t blk = bids[i];
       const bool ok = jj < nk && blk >= 0 && blk < p.num_blocks;
@@ -189,8 +206,8 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
   auto stage_tile = [&](int vb) {
     auto& vs = vs2[vb];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int pc = tid + i * 256;
+    for (int i = 0; i < NP; ++i) {
+      const int pc = tid + i * NT;
       const bool ok = (live >> i) & 1u;
       *reinterpret_cast<u32x4*>(&ks[pc >> 4][(pc & 15) * 8]) = ok ? kr[i] : zero4();
       *reinterpret_cast<u32x4*>(&vs[pc >> 4][(pc & 15) * 8]) = ok ? vr[i] : zero4();
@@ -201,33 +218,33 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
   const int first_pos = nk - nq + qt * BQ;  // the position of the tile's first query token
 
   // ---- per-tile steps of the register-staged path (padded LDS rows; V double-buffered, K single-buffered)
-  auto scores = [&](f32x4 (&sc)[4][2]) {  // S^T[key][row] = K Q^T
+  auto scores = [&](f32x4 (&sc)[4][RT]) {  // S^T[key][row] = K Q^T
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
-      sc[kt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-      sc[kt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) sc[kt][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
         const u32x4 a = *reinterpret_cast<const u32x4*>(&ks[kt * 16 + r16][kc * 32 + jq * 8]);
-        sc[kt][0] = mfma_16x16x32(a, qop[0][kc], sc[kt][0]);
-        sc[kt][1] = mfma_16x16x32(a, qop[1][kc], sc[kt][1]);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) sc[kt][rt] = mfma_16x16x32(a, qop[rt][kc], sc[kt][rt]);
       }
     }
     // keep four fragment reads in flight ahead of the MFMAs that consume them
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
     for (int i = 0; i < 12; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, RT, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 4 * RT, 0);
   };
   // The causal / length mask, only where the tile reaches past the first query's position or past the keys.
   // Key j = kv0 + kt*16 + jq*4 + rr is kept when j < nk and (causal) j <= qpos: one limit per row, relative to the
   // lane's first key, so each element costs a compare against a constant and a select.
-  auto mask = [&](f32x4 (&sc)[4][2], int kv0) {
+  auto mask = [&](f32x4 (&sc)[4][RT], int kv0) {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       const int last = (p.causal ? min(nk - 1, qpos[rt]) : nk - 1) - (kv0 + jq * 4);
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
@@ -240,19 +257,20 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
   // final 1 / l), so most tiles leave the accumulators alone. Returns whether any row of the wave moved; alpha is
   // the factor (1 for rows that did not move) that the accumulators, which still hold the previous tile's P V at
   // the old max, need once that P V has been added.
-  auto softmax = [&](f32x4 (&sc)[4][2], u32x4 (&pbo)[2][2], float (&alpha)[2]) -> bool {
+  auto softmax = [&](f32x4 (&sc)[4][RT], u32x4 (&pbo)[2][RT], float (&alpha)[RT]) -> bool {
     const float c = p.scale_log2;
-    bool up[2];
+    bool any_up = false;
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       float t = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
         t = fmaxf(t, fmaxf(fmaxf(sc[kt][rt][0], sc[kt][rt][1]), fmaxf(sc[kt][rt][2], sc[kt][rt][3])));
       const float tm = col_max4(t) * c;  // scaled (log2) units; c > 0
-      up[rt] = tm > m[rt] + 8.f;
-      alpha[rt] = up[rt] ? fast_exp2(m[rt] - tm) : 1.f;  // exp2(-inf) = 0 on a row's first update
-      m[rt] = up[rt] ? tm : m[rt];
+      const bool up = tm > m[rt] + 8.f;
+      any_up = any_up || up;
+      alpha[rt] = up ? fast_exp2(m[rt] - tm) : 1.f;  // exp2(-inf) = 0 on a row's first update
+      m[rt] = up ? tm : m[rt];
       const float mu = m[rt] == -INFINITY ? 0.f : m[rt];
       float ps = 0.f;
 #pragma unroll
@@ -270,23 +288,23 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
+      for (int rt = 0; rt < RT; ++rt)
         pbo[k2][rt] = u32x4{pack_bf16x2(sc[2 * k2][rt][0], sc[2 * k2][rt][1]),
                             pack_bf16x2(sc[2 * k2][rt][2], sc[2 * k2][rt][3]),
                             pack_bf16x2(sc[2 * k2 + 1][rt][0], sc[2 * k2 + 1][rt][1]),
                             pack_bf16x2(sc[2 * k2 + 1][rt][2], sc[2 * k2 + 1][rt][3])};
-    return __builtin_amdgcn_ballot_w64(up[0] || up[1]) != 0;
+    return __builtin_amdgcn_ballot_w64(any_up) != 0;
   };
   // Softmax against the running max as it stands (no tile max, no cross-lane step): p = exp2(s c - m). Valid
   // while every p stays <= 2^62, which the lane's partial row sums (each at least its largest term) check;
   // otherwise the caller redoes the tile through softmax (tile max, rescale). ps gets the lane's partial row sums.
   // Returns whether any lane of the wave failed the check. A tile's scores rarely pass the running max by 62
   // (log2 units) once the first tile has set it, and p of that size loses nothing in bf16 or in the fp32 sums.
-  auto softmax_fixed = [&](const f32x4 (&sc)[4][2], u32x4 (&pbo)[2][2], float (&ps)[2]) -> bool {
+  auto softmax_fixed = [&](const f32x4 (&sc)[4][RT], u32x4 (&pbo)[2][RT], float (&ps)[RT]) -> bool {
     const float c = p.scale_log2;
     bool big = false;
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       const float mu = m[rt] == -INFINITY ? 0.f : m[rt];
       float sum = 0.f;
       uint32_t pk[8];
@@ -308,7 +326,7 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
     return __builtin_amdgcn_ballot_w64(big) != 0;
   };
   // O^T[d][row] += V^T P^T over one tile; V^T from the LDS buffer vb with two transposed reads per 8-key column
-  auto pv = [&](const u32x4 (&pbi)[2][2], int vb) {
+  auto pv = [&](const u32x4 (&pbi)[2][RT], int vb) {
     auto& vs = vs2[vb];
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
@@ -320,19 +338,20 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
         const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
         const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
         const u32x4 a = u32x4{l2[0], l2[1], h2[0], h2[1]};
-        acc[dt][0] = mfma_16x16x32(a, pbi[k2][0], acc[dt][0]);
-        acc[dt][1] = mfma_16x16x32(a, pbi[k2][1], acc[dt][1]);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) acc[dt][rt] = mfma_16x16x32(a, pbi[k2][rt], acc[dt][rt]);
       }
   };
 
-  float alpha[2] = {1.f, 1.f};  // the last softmax's accumulator factors
-  bool moved = false;           // ... and whether any of them is not 1
+  float alpha[RT];     // the last softmax's accumulator factors
+  bool moved = false;  // ... and whether any of them is not 1
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) alpha[rt] = 1.f;
   auto rescale = [&]() {
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      acc[dt][0] *= alpha[0];
-      acc[dt][1] *= alpha[1];
-    }
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) acc[dt][rt] *= alpha[rt];
   };
   constexpr bool kDma = KV != kPagedPieces;
   if constexpr (kDma) {
@@ -352,11 +371,11 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
     __shared__ __attribute__((aligned(1024))) uint8_t vt0[NH][kTB];
     __shared__ __attribute__((aligned(1024))) uint8_t vt1[NH][kTB];
     const int lc = lane & 15;
-    const int fk = lrow & 15, fv = 2 * (lrow & 7);  // rows 16 i + lrow share these
+    const int fk = lrow & 15, fv = 2 * (lrow & 7);  // rows PR i + lrow share these
     const uint32_t dk_off = (uint32_t)((lrow * rs_k + ((lc ^ fk) << 3)) * 2);
     const uint32_t dv_off = (uint32_t)((lrow * rs_v + ((lc ^ fv) << 3)) * 2);
     typedef __attribute__((address_space(3))) void lvoid;
-    // Issues one tile's 4 + 4 DMA loads into (kd, vd); piece i of wave w fills rows 16 i + 4 w .. + 3. In a tile
+    // Issues one tile's NP + NP DMA loads into (kd, vd); piece i of wave w fills rows PR i + 4 w .. + 3. In a tile
     // with missing keys each piece is a raw buffer load whose descriptor covers exactly the piece's real keys: keys
     // past nk and a whole tile of an unmapped block read as zeros (the hardware's range check), so no address is
     // clamped and no tile is patched. (The buffer form also keeps the compiler's LDS wait counting exact; the global form makes it wait
@@ -381,44 +400,44 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
         const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbc), (short)0, kBK * rs_k * 2, kBufferWord3);
         const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vbc), (short)0, kBK * rs_v * 2, kBufferWord3);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lvoid*)(kdw + i * 4096), 16, dk_off, 16 * i * rs_k * 2, 0, 0);
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lvoid*)(vdw + i * 4096), 16, dv_off, 16 * i * rs_v * 2, 0, 0);
+        for (int i = 0; i < NP; ++i) {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lvoid*)(kdw + i * PR * 256), 16, dk_off, PR * i * rs_k * 2, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lvoid*)(vdw + i * PR * 256), 16, dv_off, PR * i * rs_v * 2, 0, 0);
         }
       } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int rows = __builtin_amdgcn_readfirstlane(min(max(nreal - 16 * i, 0), 16));  // real keys in the piece
-          const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbc + (int64_t)(16 * i) * rs_k * 2),
+        for (int i = 0; i < NP; ++i) {
+          const int rows = __builtin_amdgcn_readfirstlane(min(max(nreal - PR * i, 0), PR));  // real keys in the piece
+          const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbc + (int64_t)(PR * i) * rs_k * 2),
                                                             (short)0, rows * rs_k * 2, kBufferWord3);
-          const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vbc + (int64_t)(16 * i) * rs_v * 2),
+          const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vbc + (int64_t)(PR * i) * rs_v * 2),
                                                             (short)0, rows * rs_v * 2, kBufferWord3);
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lvoid*)(kdw + i * 4096), 16, dk_off, 0, 0, 0);
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lvoid*)(vdw + i * 4096), 16, dv_off, 0, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lvoid*)(kdw + i * PR * 256), 16, dk_off, 0, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lvoid*)(vdw + i * PR * 256), 16, dv_off, 0, 0, 0);
         }
       }
     };
     // K fragment (rows kt*16 + r16, chunk kc*4 + jq) at byte kt*4096 + (krd0 ^ (kc << 6))
     const uint32_t krd0 = (uint32_t)(r16 * 256 + ((jq ^ r16) << 4));
-    auto scores_d = [&](const uint8_t* kd, f32x4 (&sc)[4][2]) {
+    auto scores_d = [&](const uint8_t* kd, f32x4 (&sc)[4][RT]) {
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
-        sc[kt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-        sc[kt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) sc[kt][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kc = 0; kc < 4; ++kc) {
           const u32x4 a = *reinterpret_cast<const u32x4*>(kd + kt * 4096 + (krd0 ^ (uint32_t)(kc << 6)));
-          sc[kt][0] = mfma_16x16x32(a, qop[0][kc], sc[kt][0]);
-          sc[kt][1] = mfma_16x16x32(a, qop[1][kc], sc[kt][1]);
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) sc[kt][rt] = mfma_16x16x32(a, qop[rt][kc], sc[kt][rt]);
         }
       }
       __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, RT, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 8 * RT, 0);
     };
     // transposed V read for (dt, k2, half h): rows k2*32 + h*16 + jq*4 + r16/4, dims dt*16 + 4 (r16 & 3) .. + 3,
     // at byte k2*8192 + h*4096 + (vrd0 ^ (dt << 5))
@@ -435,14 +454,13 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
           va[dt][k2] = u32x4{lo[0], lo[1], hi[0], hi[1]};
         }
     };
-    auto pv_mfma = [&](const u32x4 (&va)[8][2], const u32x4 (&pbi)[2][2]) {
+    auto pv_mfma = [&](const u32x4 (&va)[8][2], const u32x4 (&pbi)[2][RT]) {
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-        for (int k2 = 0; k2 < 2; ++k2) {
-          acc[dt][0] = mfma_16x16x32(va[dt][k2], pbi[k2][0], acc[dt][0]);
-          acc[dt][1] = mfma_16x16x32(va[dt][k2], pbi[k2][1], acc[dt][1]);
-        }
+        for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) acc[dt][rt] = mfma_16x16x32(va[dt][k2], pbi[k2][rt], acc[dt][rt]);
     };
     // one tile: the next tile's DMA goes out first, then the scores, the softmax and P V, whose transposed V reads run
     // 16 ahead of the MFMAs that consume them (left alone, the compiler waits for each operand right after reading
@@ -453,22 +471,22 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
         dma(kn, vn, kv0 + kBK);
         fetch_bids(kv0 + 2 * kBK);
       }
-      f32x4 sc[4][2];
+      f32x4 sc[4][RT];
       scores_d(kc_, sc);
       const bool masked = kv0 + kBK > nk || (p.causal && kv0 + kBK - 1 > first_pos);
       if (masked) mask(sc, kv0);
-      u32x4 pb[2][2];
+      u32x4 pb[2][RT];
       if (kv0 == 0) {
         softmax(sc, pb, alpha);  // the accumulators are still zero: no rescale
         moved = false;
       } else {
-        float ps[2];
+        float ps[RT];
         const bool big = softmax_fixed(sc, pb, ps);
         if (__builtin_expect(big, 0)) {  // rare: a score passed the running max by more than 62: redo with its max
           moved = softmax(sc, pb, alpha);
         } else {
-          l[0] += ps[0];
-          l[1] += ps[1];
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) l[rt] += ps[rt];
           moved = false;
         }
       }
@@ -479,10 +497,10 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
       __builtin_amdgcn_sched_group_barrier(0x100, 16, 1);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * RT, 1);
         __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, 16, 1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 8 * RT, 1);
       __syncthreads();  // the next tile has landed (the barrier waits for this wave's DMA) and this one is free
     };
     if (kv_end > 0) {
@@ -514,11 +532,11 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
         load_tile(kv0 + kBK);
         fetch_bids(kv0 + 2 * kBK);
       }
-      f32x4 sc[4][2];
+      f32x4 sc[4][RT];
       scores(sc);
       const bool masked = kv0 + kBK > nk || (p.causal && kv0 + kBK - 1 > first_pos);
       if (masked) mask(sc, kv0);
-      u32x4 pb[2][2];
+      u32x4 pb[2][RT];
       if (softmax(sc, pb, alpha)) rescale();
       pv(pb, vb);
       vb ^= 1;
@@ -529,9 +547,10 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
   if constexpr (QUANT) {
     // ---- int8 epilogue: o * inv_smooth, per-token amax over all heads, rint(o / scale) ----
     const int g_rows = G;
-    float lmax[2] = {0.f, 0.f};
+    float lmax[RT];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
+      lmax[rt] = 0.f;
       const float L = col_sum4(l[rt]);
       const float inv = L > 0.f ? 1.f / L : 0.f;
 #pragma unroll
@@ -544,13 +563,13 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
     }
     __syncthreads();  // s_amax cleared (also when no key tile ran)
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-      if (row_ok[rt]) atomicMax(&s_amax[(w * 32 + rt * 16 + r16) / g_rows], __float_as_uint(lmax[rt]));
+    for (int rt = 0; rt < RT; ++rt)
+      if (row_ok[rt]) atomicMax(&s_amax[((w * RT + rt) * 16 + r16) / g_rows], __float_as_uint(lmax[rt]));
     __syncthreads();
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       if (!row_ok[rt]) continue;
-      const float scale = fmaxf(__uint_as_float(s_amax[(w * 32 + rt * 16 + r16) / g_rows]), 1e-6f) / 127.f;
+      const float scale = fmaxf(__uint_as_float(s_amax[((w * RT + rt) * 16 + r16) / g_rows]), 1e-6f) / 127.f;
       // rint(o / scale) without a division per element: x = o * (1 / scale) is within 2.5e-5 of the exact
       // quotient (|o / scale| <= 127.5, two roundings), so rint(x) is rint(o / scale) unless x lies within 1e-4 of
       // a half-integer; those rare elements take the division. Same codes as dividing every element.
@@ -577,7 +596,7 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
 
   // ---- epilogue: normalize, bf16, 4 consecutive dims per lane per d-tile ----
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
+  for (int rt = 0; rt < RT; ++rt) {
     const float L = col_sum4(l[rt]);
     if (!row_ok[rt]) continue;
     const float inv = L > 0.f ? 1.f / L : 0.f;
@@ -593,14 +612,15 @@ __global__ __launch_bounds__(QUANT ? 512 : 256, QUANT ? 1 : 2) void prefill_kern
 
 }  // namespace
 
-template <bool QUANT>
-hipError_t launch_prefill_kind(const PrefillArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
+template <bool QUANT, int NW>
+hipError_t launch_prefill_kind(const PrefillArgs& a, dim3 grid, hipStream_t stream) {
+  const dim3 block(64 * NW * (QUANT ? a.num_kv_heads : 1));
   if (!a.block_tables)
-    prefill_kernel<QUANT, kPacked><<<grid, block, 0, stream>>>(a);
+    prefill_kernel<QUANT, kPacked, NW><<<grid, block, 0, stream>>>(a);
   else if (a.block_size % kBK == 0)
-    prefill_kernel<QUANT, kPagedTiles><<<grid, block, 0, stream>>>(a);
+    prefill_kernel<QUANT, kPagedTiles, NW><<<grid, block, 0, stream>>>(a);
   else
-    prefill_kernel<QUANT, kPagedPieces><<<grid, block, 0, stream>>>(a);
+    prefill_kernel<QUANT, kPagedPieces, NW><<<grid, block, 0, stream>>>(a);
   return hipGetLastError();
 }
 
@@ -609,9 +629,11 @@ hipError_t launch_prefill(const PrefillArgs& a0, int max_seqlen_q, hipStream_t s
   const int q_tiles = (max_seqlen_q + bq - 1) / bq;
   if (q_tiles <= 0 || a0.batch <= 0) return hipSuccess;
   PrefillArgs a = a0;
-  a.xcd_order = (int64_t)q_tiles * a.batch * a.num_kv_heads >= kXcdOrderMinWorkgroups;
-  return launch_prefill_kind<false>(a, dim3((unsigned)q_tiles, (unsigned)a.batch, (unsigned)a.num_kv_heads), dim3(256),
-                                    stream);
+  const int64_t nwg = (int64_t)q_tiles * a.batch * a.num_kv_heads;
+  a.xcd_order = nwg >= kXcdOrderMinWorkgroups;
+  const dim3 grid((unsigned)q_tiles, (unsigned)a.batch, (unsigned)a.num_kv_heads);
+  if (nwg <= kSmallGridWorkgroups) return launch_prefill_kind<false, 8>(a, grid, stream);
+  return launch_prefill_kind<false, 4>(a, grid, stream);
 }
 
 hipError_t launch_prefill_int8(const PrefillArgs& a0, int max_seqlen_q, hipStream_t stream) {
@@ -621,8 +643,7 @@ hipError_t launch_prefill_int8(const PrefillArgs& a0, int max_seqlen_q, hipStrea
   if (a0.num_kv_heads < 1 || a0.num_kv_heads > 2) return hipErrorInvalidValue;
   PrefillArgs a = a0;
   a.xcd_order = (int64_t)q_tiles * a.batch >= kXcdOrderMinWorkgroups;
-  return launch_prefill_kind<true>(a, dim3((unsigned)q_tiles, (unsigned)a.batch, 1u), dim3(256 * a.num_kv_heads),
-                                   stream);
+  return launch_prefill_kind<true, 4>(a, dim3((unsigned)q_tiles, (unsigned)a.batch, 1u), stream);
 }
 
 }  // namespace vox
