@@ -140,3 +140,28 @@ def test_int8_large_ragged_grid_in_per_xcd_order():
     out = varlen_attention(q.to(DEV), k.to(DEV), v.to(DEV), cu_seqlens_q=cu.to(DEV), cu_seqlens_k=cu.to(DEV),
                            max_seqlen_q=max(lens), softmax_scale=SCALE, causal=True, quant=True)
     _check(out, ref.varlen(q.float(), cu, cu, k=k, v=v), "per-XCD order int8")
+
+
+@pytest.mark.parametrize("bs", [None, 256, 96])
+def test_int8_sixteen_row_halves_over_several_key_tiles(bs):
+    """Grids small enough for one workgroup per CU take 16-row waves (8 tokens per workgroup at 8 heads per KV
+    head): 3 causal sequences of 150-333 tokens over several key tiles, packed keys and paged caches (block size
+    256: one block id per key tile; 96: per-piece block ids), with an inv_smooth vector."""
+    gen = torch.Generator().manual_seed(76 + (bs or 0))
+    lens = [333, 150, 271]
+    T = sum(lens)
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32)
+    q = randn(gen, T, H, D)
+    inv = torch.rand(H * D, generator=gen) + 0.5
+    if bs is None:
+        k, v = randn(gen, T, HK, D), randn(gen, T, HK, D)
+        out = varlen_attention(q.to(DEV), k.to(DEV), v.to(DEV), cu_seqlens_q=cu.to(DEV), cu_seqlens_k=cu.to(DEV),
+                               max_seqlen_q=max(lens), softmax_scale=SCALE, causal=True, quant=True,
+                               inv_smooth=inv.to(DEV))
+        want = ref.varlen(q.float(), cu, cu, k=k, v=v)
+    else:
+        kc, vc, tables = paged_pool(gen, lens, sum((n + bs - 1) // bs for n in lens) + 2, block_size=bs)
+        out = paged_prefill_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), tables.to(DEV), cu.to(DEV), cu.to(DEV),
+                                      max(lens), SCALE, quant=True, inv_smooth=inv.to(DEV))
+        want = ref.varlen(q.float(), cu, cu, k_cache=kc, v_cache=vc, block_tables=tables)
+    _check(out, want, f"16-row int8, block_size {bs}", inv)

@@ -36,7 +36,7 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kBK = 64;          // keys per tile
-constexpr int kRows = 128;       // query rows per workgroup
+constexpr int kRows = 128;       // query rows per workgroup (bf16 output)
 // LDS row strides (bf16 elements) of the K and V tiles, chosen by measuring the kernel's own access patterns on
 // gfx950: the K-fragment 16-byte reads run 1.7x faster at 144 than at 136 (and 4-8x faster than at 128 or 132),
 // the transposed V reads are fastest from 152 up; the 16-byte staging writes do not care.
@@ -59,16 +59,16 @@ enum KvSource { kPacked = 0, kPagedTiles = 1, kPagedPieces = 2 };
 // NW waves per KV group, each owning RT 16-row blocks of the 128 query rows: 4 waves x 32 rows keep the LDS reads per
 // MFMA low (the largest grids); 8 waves x 16 rows halve each wave's work per key tile, which shortens a workgroup's
 // chain of key tiles (smaller grids, where the longest chains end the launch).
-template <bool QUANT, int KV, int NW>
+template <bool QUANT, int KV, int NW, int RT>
 __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 : 2) void prefill_kernel(PrefillArgs p) {
   constexpr int NH = QUANT ? 2 : 1;  // KV-group halves per workgroup
-  constexpr int RT = 8 / NW;         // 16-row blocks per wave
+  constexpr int ROWS = 16 * RT * NW;  // query rows per KV group
   constexpr int NT = 64 * NW;        // threads per KV group
   constexpr int PR = 4 * NW;         // tile rows one load instruction of the group covers (16 bytes per thread)
   constexpr int NP = kBK / PR;       // load instructions per thread per 64-key tile
   __shared__ __attribute__((aligned(16))) uint16_t ks_all[NH][kBK][kKsStride];
   __shared__ __attribute__((aligned(16))) uint16_t vs_all[NH][2][kBK][kVsStride];  // V double-buffered
-  __shared__ unsigned s_amax[QUANT ? kRows : 1];  // QUANT: per token of the tile, float bits of max |o|
+  __shared__ unsigned s_amax[QUANT ? ROWS : 1];  // QUANT: per token of the tile, float bits of max |o|
 
   // Work item (q tile, sequence, kv head). Workgroup i runs on XCD i % 8; with xcd_order each XCD gets a contiguous
   // run of work items, so the query tiles that re-read a sequence's K/V tiles find them in that XCD's L2 (the
@@ -113,7 +113,7 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
   }
   if (KV != kPacked) nk = min(nk, p.max_blocks * p.block_size);  // keys the block table can address
   const int G = p.group;
-  const int BQ = kRows / G;  // query tokens per workgroup
+  const int BQ = ROWS / G;  // query tokens per workgroup
   if (qt * BQ >= nq) return;
 
   const int tid = threadIdx.x & (NT - 1);  // thread within the half
@@ -612,15 +612,25 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
 
 }  // namespace
 
-template <bool QUANT, int NW>
+static int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+    (void)hipGetLastError();
+    cus = 256;  // MI355X
+  }
+  return cus;
+}
+
+template <bool QUANT, int NW, int RT>
 hipError_t launch_prefill_kind(const PrefillArgs& a, dim3 grid, hipStream_t stream) {
   const dim3 block(64 * NW * (QUANT ? a.num_kv_heads : 1));
   if (!a.block_tables)
-    prefill_kernel<QUANT, kPacked, NW><<<grid, block, 0, stream>>>(a);
+    prefill_kernel<QUANT, kPacked, NW, RT><<<grid, block, 0, stream>>>(a);
   else if (a.block_size % kBK == 0)
-    prefill_kernel<QUANT, kPagedTiles, NW><<<grid, block, 0, stream>>>(a);
+    prefill_kernel<QUANT, kPagedTiles, NW, RT><<<grid, block, 0, stream>>>(a);
   else
-    prefill_kernel<QUANT, kPagedPieces, NW><<<grid, block, 0, stream>>>(a);
+    prefill_kernel<QUANT, kPagedPieces, NW, RT><<<grid, block, 0, stream>>>(a);
   return hipGetLastError();
 }
 
@@ -632,18 +642,25 @@ hipError_t launch_prefill(const PrefillArgs& a0, int max_seqlen_q, hipStream_t s
   const int64_t nwg = (int64_t)q_tiles * a.batch * a.num_kv_heads;
   a.xcd_order = nwg >= kXcdOrderMinWorkgroups;
   const dim3 grid((unsigned)q_tiles, (unsigned)a.batch, (unsigned)a.num_kv_heads);
-  if (nwg <= kSmallGridWorkgroups) return launch_prefill_kind<false, 8>(a, grid, stream);
-  return launch_prefill_kind<false, 4>(a, grid, stream);
+  if (nwg <= kSmallGridWorkgroups) return launch_prefill_kind<false, 8, 1>(a, grid, stream);
+  return launch_prefill_kind<false, 4, 2>(a, grid, stream);
 }
 
 hipError_t launch_prefill_int8(const PrefillArgs& a0, int max_seqlen_q, hipStream_t stream) {
-  const int bq = kRows / a0.group;
-  const int q_tiles = (max_seqlen_q + bq - 1) / bq;
-  if (q_tiles <= 0 || a0.batch <= 0) return hipSuccess;
+  if (max_seqlen_q <= 0 || a0.batch <= 0) return hipSuccess;
   if (a0.num_kv_heads < 1 || a0.num_kv_heads > 2) return hipErrorInvalidValue;
+  // Each KV-group half: 4 waves of 16 rows (64 / G tokens per workgroup) when that grid still fits one workgroup per
+  // CU (this instance's LDS allows one), else 4 waves of 32 rows: measured, 150 streams x 5 tokens 8.9 -> 6.7 us;
+  // where the smaller tiles need a second round of workgroups (150 x 11 tokens, 44 x 46) they cost 27-40 %.
+  const int64_t tiles16 = (max_seqlen_q + 64 / a0.group - 1) / (64 / a0.group);
+  const bool r16 = 64 % a0.group == 0 && tiles16 * a0.batch <= device_cus();
+  const int bq = (r16 ? 64 : 128) / a0.group;
+  const int q_tiles = (max_seqlen_q + bq - 1) / bq;
   PrefillArgs a = a0;
   a.xcd_order = (int64_t)q_tiles * a.batch >= kXcdOrderMinWorkgroups;
-  return launch_prefill_kind<true, 4>(a, dim3((unsigned)q_tiles, (unsigned)a.batch, 1u), stream);
+  const dim3 grid((unsigned)q_tiles, (unsigned)a.batch, 1u);
+  if (r16) return launch_prefill_kind<true, 4, 1>(a, grid, stream);
+  return launch_prefill_kind<true, 4, 2>(a, grid, stream);
 }
 
 }  // namespace vox
