@@ -136,15 +136,39 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   const int H = p.num_heads;
   const int max_ctx = p.max_blocks * p.block_size;
 
-  // ---- block table into LDS and the step layout (a block-wide prefix sum over ceil(context / 64)): one round trip
+  // ---- block table into LDS and the step layout (a block-wide prefix sum over ceil(context / 64)). The lengths of
+  // the first kThreads sequences and every table entry a thread stages are loaded before any of them is waited for:
+  // one round trip (a load-then-store loop waits for each load in turn, one round trip per kThreads entries).
   const int mb = p.max_blocks;
-  if constexpr (BTL)
-    for (int i = tid; i < p.batch * mb; i += kThreads) s_bt[i] = p.block_tables[(int64_t)(i / mb) * p.bt_stride + i % mb];
+  const int ctx_first = tid < p.batch ? p.context_lens[tid] : 0;
+  if constexpr (BTL) {
+    constexpr int kPer = (kBtLds + kThreads - 1) / kThreads;  // entries per thread at most
+    const int nbt = p.batch * mb;
+    // entry i = tid + j kThreads sits at row i / mb, column i % mb; one step of kThreads entries moves the row by
+    // kThreads / mb and the column by kThreads % mb (with one carry at most)
+    const int dq = kThreads / mb, dr = kThreads % mb;
+    int row = tid / mb, col = tid % mb;
+    int vals[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      vals[j] = tid + j * kThreads < nbt ? p.block_tables[(int64_t)row * p.bt_stride + col] : 0;
+      row += dq;
+      col += dr;
+      if (col >= mb) {
+        col -= mb;
+        ++row;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+      if (tid + j * kThreads < nbt) s_bt[tid + j * kThreads] = vals[j];
+  }
   int run = 0;
   int nmax = 0;  // most steps of one sequence
   for (int base = 0; base < p.batch; base += kThreads) {
     const int bb = base + tid;
-    const int ctx = bb < p.batch ? max(0, min(p.context_lens[bb], max_ctx)) : 0;
+    const int raw = base == 0 ? ctx_first : (bb < p.batch ? p.context_lens[bb] : 0);
+    const int ctx = bb < p.batch ? max(0, min(raw, max_ctx)) : 0;
     const int n = (ctx + kStep - 1) / kStep;
     const int incl = wave_incl_scan(n, lane);
     int wmax = n;
