@@ -640,9 +640,13 @@ hipError_t launch_prefill(const PrefillArgs& a0, int max_seqlen_q, hipStream_t s
   PrefillArgs a = a0;
   // 4 waves of 16 rows (64 / G tokens per workgroup) when that grid fits two workgroups per CU at once: rows that
   // hold no query token still run every key tile, and a 128-row workgroup over a few tokens is mostly such rows
-  // (measured: head-start step 200 x 7 tokens 7.4 -> 6.8 us, LocEnc 150 x 5 6.1 -> 5.5 us)
+  // (measured: head-start step 200 x 7 tokens 7.4 -> 6.8 us, LocEnc 150 x 5 6.1 -> 5.5 us). Up to four per CU when
+  // the longest sequence spans 16+ such tiles: halving a workgroup's rows halves the work of its chain of key tiles
+  // (config 2: 16.9 -> 16.2 us), while on short sequences the doubled tile loads cost more than that saves (44 x 46
+  // tokens paged 12.8 -> 14.0 us, LocDiT 150 x 11 8.4 -> 10.0 us with the wider rule).
   const int64_t tiles64 = (max_seqlen_q + 64 / a.group - 1) / (64 / a.group);
-  if (64 % a.group == 0 && tiles64 * a.batch * a.num_kv_heads <= 2 * (int64_t)device_cus()) {
+  const int64_t grid64 = tiles64 * a.batch * a.num_kv_heads, cus = device_cus();
+  if (64 % a.group == 0 && (grid64 <= 2 * cus || (grid64 <= 4 * cus && tiles64 >= 16))) {
     a.xcd_order = 0;
     return launch_prefill_kind<false, 4, 1>(a, dim3((unsigned)tiles64, (unsigned)a.batch, (unsigned)a.num_kv_heads),
                                             stream);
