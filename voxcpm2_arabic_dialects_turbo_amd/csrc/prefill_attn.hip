@@ -664,10 +664,13 @@ hipError_t launch_prefill_int8(const PrefillArgs& a0, int max_seqlen_q, hipStrea
   if (max_seqlen_q <= 0 || a0.batch <= 0) return hipSuccess;
   if (a0.num_kv_heads < 1 || a0.num_kv_heads > 2) return hipErrorInvalidValue;
   // Each KV-group half: 4 waves of 16 rows (64 / G tokens per workgroup) when that grid still fits one workgroup per
-  // CU (this instance's LDS allows one), else 4 waves of 32 rows: measured, 150 streams x 5 tokens 8.9 -> 6.7 us;
-  // where the smaller tiles need a second round of workgroups (150 x 11 tokens, 44 x 46) they cost 27-40 %.
+  // CU (this instance's LDS allows one), or two rounds of them when the longest sequence spans 16+ such tiles (its
+  // key-tile chains are long enough to gain from half the rows), else 4 waves of 32 rows. Measured: 150 streams x 5
+  // tokens 8.9 -> 6.7 us, config 2 24.6 -> 24.0 us; where the smaller tiles need a second round of workgroups over
+  // short sequences (150 x 11 tokens, 44 x 46) they cost 27-40 %.
   const int64_t tiles16 = (max_seqlen_q + 64 / a0.group - 1) / (64 / a0.group);
-  const bool r16 = 64 % a0.group == 0 && tiles16 * a0.batch <= device_cus();
+  const int64_t grid16 = tiles16 * a0.batch, cus = device_cus();
+  const bool r16 = 64 % a0.group == 0 && (grid16 <= cus || (grid16 <= 2 * cus && tiles16 >= 16));
   const int bq = (r16 ? 64 : 128) / a0.group;
   const int q_tiles = (max_seqlen_q + bq - 1) / bq;
   PrefillArgs a = a0;
