@@ -43,7 +43,9 @@ int vox_store_kvcache(const void* key, const void* value, int64_t key_row_stride
  * softmax_scale, causal=True) (reference: nanovllm_voxcpm/model/layers.py:349-358).
  *   q            bf16 [batch, num_heads, head_dim], sequence rows q_row_stride apart, heads head_dim apart
  *   k/v_cache    bf16 [num_blocks, block_size, num_kv_heads, head_dim], contiguous
- *   block_tables int32 [batch, bt_stride]; columns >= ceil(context_lens[b] / block_size) are never read
+ *   block_tables int32 [batch, bt_stride]; the first max_blocks columns of every row must be readable (the
+ *                kernel may stage them all), but entries past ceil(context_lens[b] / block_size) are never used;
+ *                an entry inside the context outside [0, num_blocks) masks that block's keys (no weight)
  *   context_lens int32 [batch]; 0 = padded row, whose output is written as zeros
  *   workspace    >= vox_decode_workspace_bytes(batch) bytes of scratch (split-KV partials), used by the two
  *                kernels the call launches in order on `stream`

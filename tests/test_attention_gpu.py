@@ -3,6 +3,7 @@ of a small engine loop, and the decode step captured into a HIP graph and replay
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
@@ -132,3 +133,47 @@ def test_decode_step_captured_in_a_graph_replays_like_eager():
         for i, layer in enumerate(model):
             q = q_in[:n, :H * D].view(n, H, D)
             attn_close(out[i, :n].view(n, H, D), _expect(layer, q, tasks, [1] * n), f"replay {rep} layer {i}")
+
+
+@pytest.mark.parametrize("cached", [[0, 0, 0, 0], [0, 260, 100, 3]])
+def test_last_rows_through_attention_forward(cached):
+    """The residual LM's last layer (reference: kernels/fused_layer.py:749-781) through Attention.forward: the KV
+    store inside uses every row of the step (slot_mapping unchanged), while cu_seqlens_q = arange(n + 1) and
+    max_seqlen_q = 1 are set in place on the live context for the one call, with the last row of each sequence as
+    its query. Without a cached prefix the keys are the step's own rows; with one, they come through the tables."""
+    gen = torch.Generator().manual_seed(64 + sum(cached))
+    layer = Attention(H, D, SCALE, HK)
+    runner.allocate_kv_cache([layer], num_blocks=32, block_size=BS, device=DEV)
+    layer.k_cache.copy_(randn(gen, *layer.k_cache.shape).to(DEV))
+    layer.v_cache.copy_(randn(gen, *layer.v_cache.shape).to(DEV))
+    perm = torch.randperm(32, generator=gen).tolist()
+    lengths = [40, 300, 513, 7]
+    tasks, at = [], 0
+    for n, c in zip(lengths, cached):
+        nb = (n + BS - 1) // BS
+        tasks.append(runner.RunnerTask(perm[at:at + nb], n, c, BS))
+        at += nb
+    new = [n - c for n, c in zip(lengths, cached)]
+    T = sum(new)
+    runner.prepare_prefill_context(tasks, BS, device=DEV)
+    q, k, v = _step_qkv(gen, T)
+    rows = torch.tensor(np.cumsum(new) - 1, device=DEV)
+    ctx = get_context()
+    saved = ctx.cu_seqlens_q, ctx.max_seqlen_q
+    ctx.cu_seqlens_q, ctx.max_seqlen_q = torch.arange(len(tasks) + 1, dtype=torch.int32, device=DEV), 1
+    try:
+        o = layer(q[rows].contiguous(), k, v)
+    finally:
+        ctx.cu_seqlens_q, ctx.max_seqlen_q = saved
+    torch.cuda.synchronize()
+    assert o.shape == (len(tasks), H, D)
+    # every row's K/V went to its slot; the last row of each sequence attends over the sequence's whole length
+    want = _expect(layer, q[rows], tasks, [1] * len(tasks))
+    attn_close(o, want, f"last rows, cached {cached}")
+    kc = layer.k_cache.cpu()
+    at = 0
+    for t, n in zip(tasks, new):
+        got_rows = torch.stack([kc.view(-1, HK, D)[ref.slot_of(t.block_table, j, BS)]
+                                for j in range(t.num_cached_tokens, t.seq_length)])
+        assert torch.equal(got_rows, k[at:at + n].cpu()), "the store must write every row of the step"
+        at += n

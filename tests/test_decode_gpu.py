@@ -203,6 +203,37 @@ def test_decode_equals_varlen_prefill_with_one_query():
     dec = decode_attention(q, kc_d, vc_d, torch.tensor(lens, dtype=torch.int32, device=DEV), t_d, SCALE)
     cu_q = torch.arange(len(lens) + 1, dtype=torch.int32, device=DEV)
     cu_k = torch.tensor([0] + np.cumsum(lens).tolist(), dtype=torch.int32, device=DEV)
-    pre = flash_attn_varlen_func(q, kc_d, vc_d, 1, cu_q, max(lens), cu_k, softmax_scale=SCALE, causal=True,
+    pre = flash_attn_varlen_func(q, kc_d, vc_d, cu_q, cu_k, 1, max(lens), softmax_scale=SCALE, causal=True,
                                  block_table=t_d)
     attn_close(dec.float().cpu(), pre.float().cpu(), "decode vs varlen nq=1")
+
+
+def test_unmapped_blocks_inside_the_context_are_masked_like_prefill():
+    """A block-table entry inside a sequence's context that addresses no block (-1, or past the pool) takes no
+    weight in decode (expected: the oracle over the sequence without that block's keys; a fully unmapped context
+    gives zeros), and the one-query varlen prefill over the same bad table gives the same result."""
+    from voxcpm2_arabic_dialects_turbo_amd.ops import flash_attn_varlen_func
+
+    gen = torch.Generator().manual_seed(39)
+    lens = [700, 300, 200, 1000]
+    pool = 16
+    kc, vc, tables = paged_pool(gen, lens, pool)
+    bad = tables.clone()
+    bad[0, 1] = -1          # keys 256 .. 511 of sequence 0
+    bad[1, 0] = pool + 3    # keys 0 .. 255 of sequence 1
+    bad[2, 0] = -9          # all of sequence 2
+    q = randn(gen, len(lens), H, D)
+    lens_d = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    out = decode_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), lens_d, bad.to(DEV), SCALE)
+    width = tables.shape[1]
+    keep = [[int(x) for j, x in enumerate(tables[b].tolist()) if x >= 0 and bad[b, j] == x] for b in range(4)]
+    t_ref = torch.tensor([k + [-1] * (width - len(k)) for k in keep], dtype=torch.int32)
+    lens_ref = [lens[0] - 256, lens[1] - 256, 0, lens[3]]
+    want = ref.decode(q.float(), kc, vc, lens_ref, t_ref, SCALE)
+    attn_close(out, want, "decode, unmapped blocks masked")
+    assert out[2].float().abs().max().item() == 0.0
+    cu_q = torch.arange(len(lens) + 1, dtype=torch.int32, device=DEV)
+    cu_k = torch.tensor([0] + np.cumsum(lens).tolist(), dtype=torch.int32, device=DEV)
+    pre = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), cu_q, cu_k, 1, max(lens), softmax_scale=SCALE,
+                                 causal=True, block_table=bad.to(DEV))
+    attn_close(pre, out.float(), "prefill nq=1 vs decode on the same unmapped blocks")

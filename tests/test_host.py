@@ -1,4 +1,4 @@
-"""Host logic on the CPU: the context builders against the oracle's per-token loops, HostPack, KV-cache
+"""Host logic on the CPU: the context builders against the oracle's per-token loops, the staging buffer, KV-cache
 allocation, decode graph buffers, and Attention.forward's dispatch (with the kernels recorded, not run)."""
 
 from __future__ import annotations
@@ -74,18 +74,58 @@ def test_decode_context_matches_the_per_sequence_formulas(seed):
     assert got["max"] == (False, 0, 0)
 
 
-def test_host_pack_round_trips_dtypes_shapes_and_alignment():
-    pack = runner.HostPack("cpu")
+def test_step_staging_round_trips_dtypes_shapes_and_alignment():
+    stage = runner.StepStaging("cpu")
     a = np.arange(5, dtype=np.int64)
-    b = np.arange(7, dtype=np.int32).reshape(7)
+    b = np.arange(7, dtype=np.int32)
     c = np.arange(12, dtype=np.int32).reshape(3, 4) - 6
-    ia, ib, ic = pack.add(a), pack.add(b), pack.add(c)
-    views = pack.upload()
-    assert views[ia].dtype == torch.int64 and views[ia].tolist() == a.tolist()
-    assert views[ib].dtype == torch.int32 and views[ib].tolist() == b.tolist()
-    assert views[ic].shape == (3, 4) and views[ic].tolist() == c.tolist()
-    base = views[ia].data_ptr()  # parts start at 256-byte offsets of the one buffer
-    assert (views[ib].data_ptr() - base) % 256 == 0 and (views[ic].data_ptr() - base) % 256 == 0
+    va, vb, vc, ve = stage.layout([(np.int64, a.shape), (np.int32, b.shape), (np.int32, c.shape), (np.int32, (0,))])
+    va[:], vb[:], vc[...] = a, b, c
+    ta, tb, tc, te = stage.upload()
+    assert ta.dtype == torch.int64 and ta.tolist() == a.tolist()
+    assert tb.dtype == torch.int32 and tb.tolist() == b.tolist()
+    assert tc.shape == (3, 4) and tc.tolist() == c.tolist()
+    assert te.shape == (0,)
+    base = ta.data_ptr()  # arrays start at 256-byte offsets of the one buffer
+    assert (tb.data_ptr() - base) % 256 == 0 and (tc.data_ptr() - base) % 256 == 0
+    # the uploaded copy does not alias the staging buffer: refilling it leaves earlier uploads alone
+    vb2, = stage.layout([(np.int32, (7,))])
+    vb2[:] = -1
+    assert tb.tolist() == b.tolist()
+
+
+@pytest.mark.parametrize("first,count", [([3, 10, 0, 7], [2, 0, 3, 1]), ([5], [0]), ([], []), ([0, 0], [4, 4])])
+def test_runs_are_concatenated_aranges(first, count):
+    f, c = np.array(first, dtype=np.int64), np.array(count, dtype=np.int64)
+    want = [x for fi, ci in zip(first, count) for x in range(fi, fi + ci)]
+    assert runner._runs(f, c).tolist() == want
+
+
+def test_prefill_slots_with_a_prefix_ending_inside_a_block_and_sequences_without_tables():
+    """Pieces of a sequence's new tokens split at block boundaries; sequences without a table (warm-up) or without
+    new tokens add no slots."""
+    tasks = [runner.RunnerTask([9, 4, 7], 11, 3, BS), runner.RunnerTask([], 5, 0, BS),
+             runner.RunnerTask([2, 8], 6, 6, BS), runner.RunnerTask([5], 2, 0, BS)]
+    got = runner.prefill_slots(runner._Batch.of(tasks), BS).tolist()
+    want = [t.block_table[p // BS] * BS + p % BS for t in tasks if t.block_table
+            for p in range(t.num_cached_tokens, t.seq_length)]
+    assert got == want == [39, 16, 17, 18, 19, 28, 29, 30, 20, 21]
+
+
+def test_prefill_context_of_two_hundred_requests_matches_the_loop():
+    """A burst the size of the reference's host-path benchmark (200 cloned requests over a shared prefix)."""
+    rng = np.random.default_rng(7)
+    tasks = []
+    for i in range(200):
+        prefix = [1000 + j for j in range(3)]
+        length = int(rng.integers(13, 40))
+        own = list(range(4 * i, 4 * i + (length + BS - 1) // BS - 3))
+        tasks.append(runner.RunnerTask(prefix + own, length, 12, BS))
+    positions = runner.prepare_prefill_context(tasks, BS, device="cpu")
+    pos, cu_q, cu_k, max_q, max_k, slots, tables = ctxref.prefill_context(BS, tasks)
+    got = _snapshot()
+    assert positions.tolist() == pos and got["slot_mapping"] == (torch.int32, slots)
+    assert got["block_tables"] == (torch.int32, tables) and got["max"] == (True, max_q, max_k)
 
 
 def test_allocate_kv_cache_assigns_layer_views():

@@ -94,9 +94,9 @@ def test_config2_store_then_prefill(mode):
     store_kvcache(k, v, kc_d, vc_d, slots.to(DEV))
     cu = _cu(lens).to(DEV)
     if mode == "packed":
-        out = flash_attn_varlen_func(q, k, v, max(lens), cu, max(lens), cu, softmax_scale=SCALE, causal=True)
+        out = flash_attn_varlen_func(q, k, v, cu, cu, max(lens), max(lens), softmax_scale=SCALE, causal=True)
     else:
-        out = flash_attn_varlen_func(q, kc_d, vc_d, max(lens), cu, max(lens), cu, softmax_scale=SCALE, causal=True,
+        out = flash_attn_varlen_func(q, kc_d, vc_d, cu, cu, max(lens), max(lens), softmax_scale=SCALE, causal=True,
                                      block_table=tables.to(DEV))
     want = ref.varlen(q.float().cpu(), _cu(lens), _cu(lens), k=k.cpu(), v=v.cpu())
     attn_close(out, want, f"config 2 {mode}")
@@ -119,7 +119,7 @@ def test_config5_mixed_prefill_and_decode_rows():
     kc_d, vc_d = kc.to(DEV), vc.to(DEV)
     store_kvcache(k_new.to(DEV), v_new.to(DEV), kc_d, vc_d, slots.to(DEV))
     ref.store_kvcache(k_new, v_new, kc, vc, slots)
-    out = flash_attn_varlen_func(q.to(DEV), kc_d, vc_d, max(nq), _cu(nq).to(DEV), max(nk), _cu(nk).to(DEV),
+    out = flash_attn_varlen_func(q.to(DEV), kc_d, vc_d, _cu(nq).to(DEV), _cu(nk).to(DEV), max(nq), max(nk),
                                  softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
     want = ref.varlen(q.float(), _cu(nq), _cu(nk), k_cache=kc, v_cache=vc, block_tables=tables)
     attn_close(out, want, "config 5")
@@ -134,8 +134,8 @@ def test_last_rows_one_query_per_sequence_over_all_keys():
     k, v = randn(gen, T, HK, D), randn(gen, T, HK, D)
     q_last = randn(gen, len(lens), H, D)
     cu_q = torch.arange(len(lens) + 1, dtype=torch.int32)
-    out = flash_attn_varlen_func(q_last.to(DEV), k.to(DEV), v.to(DEV), 1, cu_q.to(DEV), max(lens),
-                                 _cu(lens).to(DEV), softmax_scale=SCALE, causal=True)
+    out = flash_attn_varlen_func(q_last.to(DEV), k.to(DEV), v.to(DEV), cu_q.to(DEV), _cu(lens).to(DEV), 1,
+                                 max(lens), softmax_scale=SCALE, causal=True)
     want = ref.varlen(q_last.float(), cu_q, _cu(lens), k=k, v=v)
     attn_close(out, want, "last rows")
 
@@ -147,7 +147,7 @@ def test_zero_length_sequences_in_a_padded_batch():
     nk = [0, 17, 0, 0, 300, 0]
     kc, vc, tables = paged_pool(gen, [max(n, 1) for n in nk], 16)
     q = randn(gen, sum(nq), H, D)
-    out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), 64, _cu(nq).to(DEV), 300, _cu(nk).to(DEV),
+    out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), _cu(nq).to(DEV), _cu(nk).to(DEV), 64, 300,
                                  softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
     want = ref.varlen(q.float(), _cu(nq), _cu(nk), k_cache=kc, v_cache=vc, block_tables=tables)
     attn_close(out, want, "zero-length sequences")
@@ -162,8 +162,8 @@ def test_paged_block_sizes(bs):
     nk = [37 + 90, 1 + 700, 130, 64 + 63]
     kc, vc, tables = paged_pool(gen, nk, sum((n + bs - 1) // bs for n in nk) + 3, block_size=bs)
     q = randn(gen, sum(nq), H, D)
-    out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), max(nq), _cu(nq).to(DEV), max(nk),
-                                 _cu(nk).to(DEV), softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
+    out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), _cu(nq).to(DEV), _cu(nk).to(DEV), max(nq),
+                                 max(nk), softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
     want = ref.varlen(q.float(), _cu(nq), _cu(nk), k_cache=kc, v_cache=vc, block_tables=tables)
     attn_close(out, want, f"paged block_size {bs}")
 
@@ -174,8 +174,8 @@ def test_group_sizes(h, hk):
     lens = [1, 70, 129, 33]
     T = sum(lens)
     q, k, v = randn(gen, T, h, D), randn(gen, T, hk, D), randn(gen, T, hk, D)
-    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), max(lens), _cu(lens).to(DEV), max(lens),
-                                 _cu(lens).to(DEV), softmax_scale=SCALE, causal=True)
+    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), _cu(lens).to(DEV), _cu(lens).to(DEV), max(lens),
+                                 max(lens), softmax_scale=SCALE, causal=True)
     attn_close(out, ref.varlen(q.float(), _cu(lens), _cu(lens), k=k, v=v), f"H={h} HK={hk}")
 
 
@@ -185,8 +185,8 @@ def test_long_sequences_compute_bound_shape():
     lens = uniform_lens(gen, 4, 1024, 2048)
     T = sum(lens)
     q, k, v = randn(gen, T, H, D), randn(gen, T, HK, D), randn(gen, T, HK, D)
-    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), max(lens), _cu(lens).to(DEV), max(lens),
-                                 _cu(lens).to(DEV), softmax_scale=SCALE, causal=True)
+    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), _cu(lens).to(DEV), _cu(lens).to(DEV), max(lens),
+                                 max(lens), softmax_scale=SCALE, causal=True)
     attn_close(out, ref.varlen(q.float(), _cu(lens), _cu(lens), k=k, v=v), "long causal")
 
 
@@ -198,8 +198,8 @@ def test_prefill_closed_forms_identical_keys():
     T = sum(lens)
     q, v = randn(gen, T, H, D), randn(gen, T, HK, D)
     k = randn(gen, 1, HK, D).expand(T, HK, D).contiguous()
-    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), max(lens), _cu(lens).to(DEV), max(lens),
-                                 _cu(lens).to(DEV), softmax_scale=SCALE, causal=True).float().cpu()
+    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), _cu(lens).to(DEV), _cu(lens).to(DEV), max(lens),
+                                 max(lens), softmax_scale=SCALE, causal=True).float().cpu()
     at = 0
     for n in lens:
         vs = v[at:at + n].float()
@@ -228,7 +228,7 @@ def test_prefill_scores_growing_across_key_tiles():
         k[j] = u * (0.05 * (j - 63))
     k = k.to(torch.bfloat16)
     cu = _cu([L])
-    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), L, cu.to(DEV), L, cu.to(DEV), softmax_scale=SCALE,
+    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), cu.to(DEV), cu.to(DEV), L, L, softmax_scale=SCALE,
                                  causal=True)
     want = ref.varlen(q.float(), cu, cu, k=k, v=v)
     assert torch.isfinite(out.float()).all()
@@ -237,20 +237,28 @@ def test_prefill_scores_growing_across_key_tiles():
     for j in range(L):
         kc[tables[0, j // BLOCK], j % BLOCK] = k[j]
         vc[tables[0, j // BLOCK], j % BLOCK] = v[j]
-    out2 = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), L, cu.to(DEV), L, cu.to(DEV),
+    out2 = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), cu.to(DEV), cu.to(DEV), L, L,
                                   softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
     attn_close(out2, want, "growing scores, paged")
 
 
+def _without_columns(table, drop, width):
+    """A block-table row without the given columns, -1 padded to ``width``."""
+    kept = [int(x) for j, x in enumerate(table.tolist()) if j not in drop and x >= 0]
+    return kept + [-1] * (width - len(kept))
+
+
 @pytest.mark.parametrize("bs", [256, 32])
-def test_paged_unmapped_blocks_read_as_zeros_and_slots_past_the_keys_stay_unread(bs):
-    """Block-table entries that address no block (-1, or past the pool) read as zero keys and values, and cache slots
-    past a sequence's keys are never used: they hold NaN here, and the output stays finite and equal to the oracle's
-    over a cache in which those entries point at an all-zero block. 256: the tiles that go straight to LDS (range-
-    checked loads); 32: the register-staged per-piece path."""
+def test_paged_unmapped_blocks_are_masked_and_slots_past_the_keys_stay_unread(bs):
+    """Block-table entries inside a sequence's context that address no block (-1, or past the pool) are masked:
+    their keys take no weight, as in the decode kernel. Expected: the oracle over the same sequence with those
+    blocks' keys removed (each such block lies wholly inside the cached prefix, before the first query's position,
+    so every query would have seen all of its keys and the causal alignment of the others is unchanged); a sequence
+    whose whole context is unmapped gives zeros. Cache slots past a sequence's keys hold NaN and are never used.
+    256: the tiles that go straight to LDS (range-checked loads); 32: the register-staged per-piece path."""
     gen = torch.Generator().manual_seed(71 + bs)
-    nq = [50, 3, 129]
-    nk = [50 + 600, 3 + 300, 129 + 40]
+    nq = [50, 3, 20]
+    nk = [50 + 600, 3 + 300, 20 + 40]
     pool = sum((n + bs - 1) // bs for n in nk) + 2
     kc, vc, tables = paged_pool(gen, nk, pool, block_size=bs)
     for b, n in enumerate(nk):  # NaN in every slot past the sequence's keys
@@ -258,20 +266,23 @@ def test_paged_unmapped_blocks_read_as_zeros_and_slots_past_the_keys_stay_unread
             used = min(bs, n - j * bs)
             kc[tables[b, j], used:] = float("nan")
             vc[tables[b, j], used:] = float("nan")
-    zero_id = pool  # the oracle's all-zero block
-    kc_ref = torch.cat([kc, torch.zeros(1, bs, HK, D, dtype=kc.dtype)])
-    vc_ref = torch.cat([vc, torch.zeros(1, bs, HK, D, dtype=vc.dtype)])
-    t_ref = tables.clone()
     t_gpu = tables.clone()
-    for b, j, bad in [(0, 1, -1), (1, 0, pool + 5), (2, 0, -7)]:  # one unmapped block per sequence
-        t_gpu[b, j] = bad
-        t_ref[b, j] = zero_id
+    t_gpu[0, 1] = -1            # keys bs .. 2 bs - 1 of sequence 0 (inside its 600-token prefix)
+    t_gpu[1, 0] = pool + 5      # keys 0 .. bs - 1 of sequence 1 (inside its 300-token prefix)
+    whole = (nk[2] + bs - 1) // bs
+    t_gpu[2, :whole] = -7       # every key of sequence 2
     q = randn(gen, sum(nq), H, D)
-    out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), max(nq), _cu(nq).to(DEV), max(nk),
-                                 _cu(nk).to(DEV), softmax_scale=SCALE, causal=True, block_table=t_gpu.to(DEV))
+    out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), _cu(nq).to(DEV), _cu(nk).to(DEV), max(nq),
+                                 max(nk), softmax_scale=SCALE, causal=True, block_table=t_gpu.to(DEV))
     assert torch.isfinite(out.float()).all()
-    want = ref.varlen(q.float(), _cu(nq), _cu(nk), k_cache=kc_ref, v_cache=vc_ref, block_tables=t_ref)
-    attn_close(out, want, f"unmapped blocks, block_size {bs}")
+    width = tables.shape[1]
+    t_ref = torch.tensor([_without_columns(tables[0], {1}, width), _without_columns(tables[1], {0}, width)],
+                         dtype=torch.int32)
+    nk_ref = [nk[0] - bs, nk[1] - bs]
+    want = ref.varlen(q[:nq[0] + nq[1]].float(), _cu(nq[:2]), _cu(nk_ref), k_cache=kc, v_cache=vc,
+                      block_tables=t_ref)
+    attn_close(out[:nq[0] + nq[1]], want, f"unmapped blocks masked, block_size {bs}")
+    assert out[nq[0] + nq[1]:].float().abs().max().item() == 0.0, "a fully unmapped context gives zeros"
 
 
 def test_large_ragged_grid_in_per_xcd_order():
@@ -281,15 +292,15 @@ def test_large_ragged_grid_in_per_xcd_order():
     lens = [2048, 100, 1500, 7, 900, 2047, 64, 1300]
     T = sum(lens)
     q, k, v = randn(gen, T, H, D), randn(gen, T, HK, D), randn(gen, T, HK, D)
-    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), max(lens), _cu(lens).to(DEV), max(lens),
-                                 _cu(lens).to(DEV), softmax_scale=SCALE, causal=True)
+    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), _cu(lens).to(DEV), _cu(lens).to(DEV), max(lens),
+                                 max(lens), softmax_scale=SCALE, causal=True)
     want = ref.varlen(q.float(), _cu(lens), _cu(lens), k=k, v=v)
     attn_close(out, want, "per-XCD order, packed")
     nq = [max(1, n // 3) for n in lens]  # new tokens over cached prefixes
     kc, vc, tables = paged_pool(gen, lens, sum((n + BLOCK - 1) // BLOCK for n in lens) + 4)
     qp = randn(gen, sum(nq), H, D)
-    outp = flash_attn_varlen_func(qp.to(DEV), kc.to(DEV), vc.to(DEV), max(nq), _cu(nq).to(DEV), max(lens),
-                                  _cu(lens).to(DEV), softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
+    outp = flash_attn_varlen_func(qp.to(DEV), kc.to(DEV), vc.to(DEV), _cu(nq).to(DEV), _cu(lens).to(DEV), max(nq),
+                                  max(lens), softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
     wantp = ref.varlen(qp.float(), _cu(nq), _cu(lens), k_cache=kc, v_cache=vc, block_tables=tables)
     attn_close(outp, wantp, "per-XCD order, paged")
 
@@ -317,13 +328,32 @@ def test_grid_above_the_eight_wave_limit(bs):
     q = randn(gen, T, H, D)
     if bs is None:
         k, v = randn(gen, T, HK, D), randn(gen, T, HK, D)
-        out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), max(lens), _cu(lens).to(DEV), max(lens),
-                                     _cu(lens).to(DEV), softmax_scale=SCALE, causal=True)
+        out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), _cu(lens).to(DEV), _cu(lens).to(DEV), max(lens),
+                                     max(lens), softmax_scale=SCALE, causal=True)
         want = ref.varlen(q.float(), _cu(lens), _cu(lens), k=k, v=v)
     else:
         kc, vc, tables = paged_pool(gen, lens, sum((n + bs - 1) // bs for n in lens) + 2, block_size=bs)
-        out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), max(lens), _cu(lens).to(DEV), max(lens),
-                                     _cu(lens).to(DEV), softmax_scale=SCALE, causal=True,
+        out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), _cu(lens).to(DEV), _cu(lens).to(DEV), max(lens),
+                                     max(lens), softmax_scale=SCALE, causal=True,
                                      block_table=tables.to(DEV))
         want = ref.varlen(q.float(), _cu(lens), _cu(lens), k_cache=kc, v_cache=vc, block_tables=tables)
     attn_close(out, want, f"4-wave grid, block_size {bs}")
+
+
+@pytest.mark.parametrize("bs", [256, 32])
+def test_paged_gather_is_bit_exact_where_a_query_sees_one_key(bs):
+    """Paged prefill without a prefix, through a shuffled block table: query 0 of every sequence sees only key 0, so
+    its output is that key's V row exactly (p = 1), bit for bit, wherever the table put the block. 256: tiles straight
+    to LDS; 32: the per-piece path."""
+    gen = torch.Generator().manual_seed(80 + bs)
+    lens = [1, 64, 300, 33, 257]
+    pool = sum((n + bs - 1) // bs for n in lens) + 5
+    kc, vc, tables = paged_pool(gen, lens, pool, block_size=bs)
+    q = randn(gen, sum(lens), H, D)
+    out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), _cu(lens).to(DEV), _cu(lens).to(DEV), max(lens),
+                                 max(lens), softmax_scale=SCALE, causal=True, block_table=tables.to(DEV)).cpu()
+    at = 0
+    for b, n in enumerate(lens):
+        v0 = vc[int(tables[b, 0]), 0]  # [HK, D]: key 0 of sequence b
+        assert torch.equal(out[at], v0.repeat_interleave(H // HK, dim=0)), f"sequence {b}: query 0 != V[key 0]"
+        at += n

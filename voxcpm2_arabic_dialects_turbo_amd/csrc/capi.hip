@@ -71,7 +71,7 @@ int vox_decode_workgroups(void) {
     (void)hipGetLastError();
     cus = 256;  // MI355X
   }
-  return cus;  // the split kernel's resident capacity: one 8-wave workgroup per CU
+  return cus;  // one 4-wave workgroup per CU: the split kernel's ranges are balanced over every CU
 }
 
 void vox_set_decode_workgroups(int workgroups) { g_decode_grid_override = workgroups > 0 ? workgroups : 0; }

@@ -70,6 +70,8 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
   __shared__ __attribute__((aligned(16))) uint16_t ks_all[NH][kBK][kKsStride];
   __shared__ __attribute__((aligned(16))) uint16_t vs_all[NH][2][kBK][kVsStride];  // V double-buffered
   __shared__ unsigned s_amax[QUANT ? ROWS : 1];  // QUANT: per token of the tile, float bits of max |o|
+  // per-piece path: whether each key of the staged tile lies in a mapped block (an unmapped block's keys are masked)
+  __shared__ __attribute__((aligned(16))) unsigned char s_keyok[NH][KV == kPagedPieces ? kBK : 4];
 
   // Work item (q tile, sequence, kv head). Workgroup i runs on XCD i % 8; with xcd_order each XCD gets a contiguous
   // run of work items, so the query tiles that re-read a sequence's K/V tiles find them in that XCD's L2 (the
@@ -189,19 +191,24 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
     }
   };
   // register-staged loads (block sizes that are not a multiple of 64): unconditional and in bounds (a key past nk
-  // reads the sequence's last key, an unmapped block reads block 0; both are zeroed when staged)
+  // reads the sequence's last key, an unmapped block reads block 0; both are zeroed when staged, and the keys of an
+  // unmapped block are flagged for the mask)
+  unsigned mapped = 0;         // bit i: piece i's block is mapped
   auto load_tile = [&](int kv0) {
     live = 0;
+    mapped = 0;
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
       const int jj = kv0 + lrow + PR * i;
       const int jc = min(jj, nk - 1);
       const int64_t blk = bids[i];
-      const bool ok = jj < nk && blk >= 0 && blk < p.num_blocks;
+      const bool inb = blk >= 0 && blk < p.num_blocks;
+      const bool ok = jj < nk && inb;
       const int64_t off = (((ok ? blk : 0) * p.block_size + jc % p.block_size) * HK + g) * kD + dc;
       kr[i] = ld_g16(p.k_cache + off);
       vr[i] = ld_g16(p.v_cache + off);
       live |= (ok ? 1u : 0u) << i;
+      mapped |= (inb ? 1u : 0u) << i;
     }
   };
   auto stage_tile = [&](int vb) {
@@ -212,6 +219,8 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
       const bool ok = (live >> i) & 1u;
       *reinterpret_cast<u32x4*>(&ks[pc >> 4][(pc & 15) * 8]) = ok ? kr[i] : zero4();
       *reinterpret_cast<u32x4*>(&vs[pc >> 4][(pc & 15) * 8]) = ok ? vr[i] : zero4();
+      if constexpr (KV == kPagedPieces)
+        if ((pc & 15) == 0) s_keyok[half][pc >> 4] = (unsigned char)((mapped >> i) & 1u);
     }
   };
   // this lane's transposed-read address inside a 16-key x 16-d block: row jq*4 + r16/4, column 4*(r16%4)
@@ -381,6 +390,7 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
     // past nk and a whole tile of an unmapped block read as zeros (the hardware's range check), so no address is
     // clamped and no tile is patched. (The buffer form also keeps the compiler's LDS wait counting exact; the global form makes it wait
     // for every LDS read to finish.)
+    bool dma_mapped = true;  // whether the most recently loaded tile's block is mapped
     auto dma = [&](uint8_t* kd, uint8_t* vd, int kv0) {
       const char* kbc;
       const char* vbc;
@@ -394,6 +404,7 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
         kbc = reinterpret_cast<const char*>(p.k_cache + row0 * rs_k + g * kD);
         vbc = reinterpret_cast<const char*>(p.v_cache + row0 * rs_k + g * kD);
         if (!okb) nreal = 0;
+        dma_mapped = okb;
       }
       uint8_t* kdw = kd + w * 1024;
       uint8_t* vdw = vd + w * 1024;
@@ -468,6 +479,7 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
     // it); the next tile has landed by the barrier
     auto step = [&](int kv0, const uint8_t* kc_, const uint8_t* vc_, uint8_t* kn, uint8_t* vn) {
       const bool has_next = kv0 + kBK < kv_end;
+      const bool mapped_here = dma_mapped;  // this tile was the last one loaded
       if (has_next) {
         dma(kn, vn, kv0 + kBK);
         fetch_bids(kv0 + 2 * kBK);
@@ -476,6 +488,12 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
       scores_d(kc_, sc);
       const bool masked = kv0 + kBK > nk || (p.causal && kv0 + kBK - 1 > first_pos);
       if (masked) mask(sc, kv0);
+      if (__builtin_expect(!mapped_here, 0)) {  // a tile of an unmapped block (read as zeros) takes no weight
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) sc[kt][rt] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      }
       u32x4 pb[2][RT];
       if (kv0 == 0) {
         softmax(sc, pb, alpha);  // the accumulators are still zero: no rescale
@@ -537,6 +555,14 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
       scores(sc);
       const bool masked = kv0 + kBK > nk || (p.causal && kv0 + kBK - 1 > first_pos);
       if (masked) mask(sc, kv0);
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {  // keys kt*16 + jq*4 + [0, 4) of an unmapped block take no weight
+        const uint32_t ok4 = *reinterpret_cast<const uint32_t*>(&s_keyok[half][kt * 16 + jq * 4]);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) sc[kt][rt][rr] = ((ok4 >> (8 * rr)) & 1u) ? sc[kt][rt][rr] : -INFINITY;
+      }
       u32x4 pb[2][RT];
       if (softmax(sc, pb, alpha)) rescale();
       pv(pb, vb);
@@ -644,9 +670,10 @@ hipError_t launch_prefill(const PrefillArgs& a0, int max_seqlen_q, hipStream_t s
   // the longest sequence spans 16+ such tiles: halving a workgroup's rows halves the work of its chain of key tiles
   // (config 2: 16.9 -> 16.2 us), while on short sequences the doubled tile loads cost more than that saves (44 x 46
   // tokens paged 12.8 -> 14.0 us, LocDiT 150 x 11 8.4 -> 10.0 us with the wider rule).
-  const int64_t tiles64 = (max_seqlen_q + 64 / a.group - 1) / (64 / a.group);
+  const bool fits64 = 64 % a.group == 0;  // group sizes above 64 take the 128-row form only
+  const int64_t tiles64 = fits64 ? (max_seqlen_q + 64 / a.group - 1) / (64 / a.group) : 0;
   const int64_t grid64 = tiles64 * a.batch * a.num_kv_heads, cus = device_cus();
-  if (64 % a.group == 0 && (grid64 <= 2 * cus || (grid64 <= 4 * cus && tiles64 >= 16))) {
+  if (fits64 && (grid64 <= 2 * cus || (grid64 <= 4 * cus && tiles64 >= 16))) {
     a.xcd_order = 0;
     return launch_prefill_kind<false, 4, 1>(a, dim3((unsigned)tiles64, (unsigned)a.batch, (unsigned)a.num_kv_heads),
                                             stream);
@@ -668,9 +695,10 @@ hipError_t launch_prefill_int8(const PrefillArgs& a0, int max_seqlen_q, hipStrea
   // key-tile chains are long enough to gain from half the rows), else 4 waves of 32 rows. Measured: 150 streams x 5
   // tokens 8.9 -> 6.7 us, config 2 24.6 -> 24.0 us; where the smaller tiles need a second round of workgroups over
   // short sequences (150 x 11 tokens, 44 x 46) they cost 27-40 %.
-  const int64_t tiles16 = (max_seqlen_q + 64 / a0.group - 1) / (64 / a0.group);
+  const bool fits64 = 64 % a0.group == 0;  // group sizes above 64 take the 32-row form only
+  const int64_t tiles16 = fits64 ? (max_seqlen_q + 64 / a0.group - 1) / (64 / a0.group) : 0;
   const int64_t grid16 = tiles16 * a0.batch, cus = device_cus();
-  const bool r16 = 64 % a0.group == 0 && (grid16 <= cus || (grid16 <= 2 * cus && tiles16 >= 16));
+  const bool r16 = fits64 && (grid16 <= cus || (grid16 <= 2 * cus && tiles16 >= 16));
   const int bq = (r16 ? 64 : 128) / a0.group;
   const int q_tiles = (max_seqlen_q + bq - 1) / bq;
   PrefillArgs a = a0;

@@ -63,6 +63,8 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
         raise TypeError(f"store_kvcache: 16-bit key/value matching the cache dtype, got {key.dtype}/{k_cache.dtype}")
     if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
         raise ValueError("store_kvcache: caches must be contiguous [num_blocks, block_size, HK, head_dim]")
+    if k_cache.shape != v_cache.shape:
+        raise ValueError(f"store_kvcache: k_cache {tuple(k_cache.shape)} and v_cache {tuple(v_cache.shape)} differ")
     slots = _as_i32(slot_mapping.reshape(-1), "slot_mapping")
     lib = _lib.load()
     _lib.check(lib.vox_store_kvcache(key.data_ptr(), value.data_ptr(), key.stride(0), value.stride(0),
@@ -216,12 +218,33 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor | None, v: torch.Tensor | 
 
 # --------------------------------------------------------------------------------------------------------------------
 # The flash-attn entry points the reference's Attention.forward calls
+#
+# Same names, parameter order and defaults as flash-attn 2.8.3 (the version the reference pins: setup.sh:14,
+# Dockerfile:37), so positional and keyword callers both bind as they do against flash-attn. Options this path
+# does not implement (dropout, sliding windows, softcapping, ALiBi, returning probabilities or the LSE, appending new
+# keys in flash_attn_with_kvcache) raise NotImplementedError when set to anything but their inactive default.
 
 
-def flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q, max_seqlen_k, cu_seqlens_k, softmax_scale=None,
-                           causal=False, block_table=None):
+def _unsupported(fn: str, **opts) -> None:
+    """Raises for any flash-attn option given a value other than its inactive default."""
+    inactive = {"dropout_p": 0.0, "window_size": (-1, -1), "softcap": 0.0, "alibi_slopes": None,
+                "return_attn_probs": False, "k": None, "v": None, "rotary_cos": None, "rotary_sin": None,
+                "cache_batch_idx": None, "cache_leftpad": None, "return_softmax_lse": False}
+    for name, value in opts.items():
+        want = inactive[name]
+        same = value is None if want is None else (tuple(value) == want if isinstance(want, tuple) else value == want)
+        if not same:
+            raise NotImplementedError(f"{fn}: {name}={value!r} is not supported (only {want!r})")
+
+
+def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, dropout_p=0.0,
+                           softmax_scale=None, causal=False, window_size=(-1, -1), softcap=0.0, alibi_slopes=None,
+                           deterministic=False, return_attn_probs=False, block_table=None):
     """q [T, H, D]; k / v packed [Tk, HK, D], or the paged caches [num_blocks, block_size, HK, D] with
-    block_table [B, max_blocks]. Returns o [T, H, D]. (Reference call: nanovllm_voxcpm/model/layers.py:337-348.)"""
+    block_table [B, max_blocks]. Returns o [T, H, D]. The kernel is deterministic whatever ``deterministic`` says.
+    (Reference call: nanovllm_voxcpm/model/layers.py:337-348.)"""
+    _unsupported("flash_attn_varlen_func", dropout_p=dropout_p, window_size=window_size, softcap=softcap,
+                 alibi_slopes=alibi_slopes, return_attn_probs=return_attn_probs)
     scale = q.shape[-1] ** -0.5 if softmax_scale is None else softmax_scale
     if block_table is not None:
         return varlen_attention(q, None, None, cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_seqlens_k,
@@ -231,14 +254,22 @@ def flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q, max_seqlen_k, cu
                             softmax_scale=scale, causal=causal)
 
 
-def flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=None, block_table=None, softmax_scale=None,
-                            causal=False):
-    """q [B, Lq, H, D] over the paged caches; cache_seqlens int32 [B] counts every key (cached + new); returns
-    o [B, Lq, H, D]. Lq == 1 (the engine's decode) runs the split-KV decode kernel; Lq > 1 runs the varlen kernel
-    with bottom-right causal alignment. (Reference call: nanovllm_voxcpm/model/layers.py:350-358.)"""
+def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, rotary_cos=None, rotary_sin=None,
+                            cache_seqlens=None, cache_batch_idx=None, cache_leftpad=None, block_table=None,
+                            softmax_scale=None, causal=False, window_size=(-1, -1), softcap=0.0,
+                            rotary_interleaved=True, alibi_slopes=None, num_splits=0, return_softmax_lse=False):
+    """q [B, Lq, H, D] over the paged caches; cache_seqlens (int32 [B], or one int for every sequence) counts every
+    key; returns o [B, Lq, H, D]. Lq == 1 (the engine's decode) runs the split-KV decode kernel, which picks its
+    own split (``num_splits`` is not used); Lq > 1 runs the varlen kernel with bottom-right causal alignment.
+    (Reference call: nanovllm_voxcpm/model/layers.py:350-358.)"""
+    _unsupported("flash_attn_with_kvcache", k=k, v=v, rotary_cos=rotary_cos, rotary_sin=rotary_sin,
+                 cache_batch_idx=cache_batch_idx, cache_leftpad=cache_leftpad, window_size=window_size,
+                 softcap=softcap, alibi_slopes=alibi_slopes, return_softmax_lse=return_softmax_lse)
     if block_table is None or cache_seqlens is None:
         raise NotImplementedError("flash_attn_with_kvcache: the paged form (block_table, cache_seqlens) is supported")
     B, Lq, H, D = q.shape
+    if isinstance(cache_seqlens, int):
+        cache_seqlens = torch.full((B,), cache_seqlens, dtype=torch.int32, device=q.device)
     scale = D ** -0.5 if softmax_scale is None else softmax_scale
     if Lq == 1:
         return decode_attention(q[:, 0], k_cache, v_cache, cache_seqlens, block_table, scale).unsqueeze(1)
@@ -263,9 +294,12 @@ def _token_rows(x: torch.Tensor) -> torch.Tensor:
     return x.as_strided((B * L, Hx, D), (row, x.stride(2), x.stride(3)))
 
 
-def flash_attn_func(q, k, v, softmax_scale=None, causal=False):
+def flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False, window_size=(-1, -1), softcap=0.0,
+                    alibi_slopes=None, deterministic=False, return_attn_probs=False):
     """Dense attention q [B, L, H, D], k / v [B, Lk, HK, D] (the non-causal branch of Attention.forward: LocEnc and
     LocDiT rows). Returns o [B, L, H, D]. (Reference call: nanovllm_voxcpm/model/layers.py:359-361.)"""
+    _unsupported("flash_attn_func", dropout_p=dropout_p, window_size=window_size, softcap=softcap,
+                 alibi_slopes=alibi_slopes, return_attn_probs=return_attn_probs)
     B, L, H, D = q.shape
     Lk = k.shape[1]
     scale = D ** -0.5 if softmax_scale is None else softmax_scale
