@@ -185,6 +185,185 @@ def bench_decode(args, dev):
     return res
 
 
+def _rand_bf16(shape, seed, dev):
+    import torch
+
+    return torch.randn(*shape, generator=torch.Generator(device=dev).manual_seed(seed), device=dev).to(torch.bfloat16)
+
+
+def bench_config3(dev):
+    """Benchmark config 3: one decode call over 40 sequences, contexts U[200, 1500], each input set with its own
+    1024-block pool (bf16 K and V planes of [1024, 256, 2, 128]) and block tables of non-overlapping ids from a
+    shuffled pool; 10 sets (>= 350 MB read per rotation) so the Infinity Cache cannot serve them."""
+    import torch
+
+    from voxcpm2_arabic_dialects_turbo_amd.ops import decode_attention
+
+    B, POOL, SETS = 40, 1024, 10
+    gen = torch.Generator().manual_seed(30)
+    lens = torch.randint(200, 1501, (B,), generator=gen).tolist()
+    width = max((n + BS - 1) // BS for n in lens)
+    tables = []
+    for _ in range(SETS):
+        perm = torch.randperm(POOL, generator=gen).tolist()
+        t, at = torch.full((B, width), -1, dtype=torch.int32), 0
+        for b, n in enumerate(lens):
+            nb = (n + BS - 1) // BS
+            t[b, :nb] = torch.tensor(perm[at:at + nb], dtype=torch.int32)
+            at += nb
+        tables.append(t.to(dev))
+    kv = _rand_bf16((SETS, 2, POOL, BS, HK, D), 31, dev)
+    q = _rand_bf16((SETS, B, H, D), 32, dev)
+    lens_d = torch.tensor(lens, dtype=torch.int32, device=dev)
+    out = torch.empty(B, H, D, dtype=torch.bfloat16, device=dev)
+
+    def run():
+        for i in range(SETS):
+            decode_attention(q[i], kv[i, 0], kv[i, 1], lens_d, tables[i], SCALE, out=out)
+
+    ms = _graph_ms(run, 20) / SETS
+    nbytes = decode_bytes(lens)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    del kv
+    return dict(workload="BASELINE config 3: decode, 40 seqs, ctx U[200,1500], 1024-block pool, one layer",
+                launch_us=round(ms * 1e3, 2), launch_bytes=nbytes, gbs=round(gbs, 1),
+                frac_hbm_peak=round(gbs / HBM_PEAK_GBS, 4), input_sets=SETS)
+
+
+def bench_config5(dev):
+    """Benchmark config 5: a mixed chunked-prefill + decode step in one varlen paged call. 6 new prefills of U[300,
+    600] tokens (no cached prefix) and 120 decode rows (one new token over U[128, 1800] cached ones), in the
+    scheduler's order (prefills, then the decode riders); the step's new K/V rows (every prefill token and each
+    decode row's token) are stored first through store_kvcache, as Attention.forward does. 2048-block pool (bf16 K and
+    V planes [2048, 256, 2, 128]); 3 input sets on disjoint blocks (>= 440 MB read per rotation). Reports the step
+    (store + attention, Attention.forward) and the attention launch alone against its roofline
+    max(bytes / HBM peak, flops / MFMA peak)."""
+    import torch
+
+    from voxcpm2_arabic_dialects_turbo_amd.context import reset_context, set_context
+    from voxcpm2_arabic_dialects_turbo_amd.layers import Attention
+    from voxcpm2_arabic_dialects_turbo_amd.ops import varlen_attention
+
+    POOL, SETS = 2048, 3
+    gen = torch.Generator().manual_seed(51)
+    pre = torch.randint(300, 601, (6,), generator=gen).tolist()
+    dec = torch.randint(128, 1801, (120,), generator=gen).tolist()
+    nk = pre + dec
+    nq = pre + [1] * len(dec)
+    width = max((n + BS - 1) // BS for n in nk)
+    perm = torch.randperm(POOL, generator=gen).tolist()
+    tables, slots, at = [], [], 0
+    for _ in range(SETS):
+        t = torch.full((len(nk), width), -1, dtype=torch.int32)
+        sl = []
+        for b, n in enumerate(nk):
+            nb = (n + BS - 1) // BS
+            ids = perm[at:at + nb]
+            at += nb
+            t[b, :nb] = torch.tensor(ids, dtype=torch.int32)
+            sl += [ids[j // BS] * BS + j % BS for j in range(n - nq[b], n)]
+        tables.append(t.to(dev))
+        slots.append(torch.tensor(sl, dtype=torch.int32, device=dev))
+    assert at <= POOL
+    T = sum(nq)
+    layer = Attention(H, D, SCALE, HK)
+    kv = _rand_bf16((2, POOL, BS, HK, D), 52, dev)
+    layer.k_cache, layer.v_cache = kv[0], kv[1]
+    qkv = _rand_bf16((SETS, T, (H + 2 * HK) * D), 53, dev)
+    cu_q = torch.tensor([0] + torch.tensor(nq).cumsum(0).tolist(), dtype=torch.int32, device=dev)
+    cu_k = torch.tensor([0] + torch.tensor(nk).cumsum(0).tolist(), dtype=torch.int32, device=dev)
+    o = torch.empty(T, H, D, dtype=torch.bfloat16, device=dev)
+
+    def views(i):
+        q, k, v = qkv[i].split([H * D, HK * D, HK * D], dim=-1)
+        return q.view(T, H, D), k.view(T, HK, D), v.view(T, HK, D)
+
+    def run_step():
+        for i in range(SETS):
+            set_context(True, cu_q, cu_k, max(nq), max(nk), slots[i], None, tables[i])
+            q, k, v = views(i)
+            layer(q, k, v)
+
+    def run_attn():
+        for i in range(SETS):
+            varlen_attention(views(i)[0], None, None, cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, max_seqlen_q=max(nq),
+                             softmax_scale=SCALE, causal=True, block_table=tables[i], k_cache=kv[0], v_cache=kv[1],
+                             out=o)
+
+    try:
+        step_ms = _graph_ms(run_step, 20) / SETS
+    finally:
+        reset_context()
+    ms = _graph_ms(run_attn, 20) / SETS
+    flops, nbytes = prefill_units(nq, nk)
+    t_roof = max(nbytes / (HBM_PEAK_GBS * 1e9), flops / (MFMA_BF16_PEAK_TFLOPS * 1e12))
+    del kv, qkv
+    return dict(workload="BASELINE config 5: one varlen paged call, 6 prefills U[300,600] + 120 decode rows "
+                         "ctx U[128,1800], 2048-block pool",
+                step_us=round(step_ms * 1e3, 2), launch_us=round(ms * 1e3, 2), flops=flops, bytes=nbytes,
+                tflops=round(flops / (ms * 1e-3) / 1e12, 2), gbs=round(nbytes / (ms * 1e-3) / 1e9, 1),
+                pct_mfma_peak=round(100 * flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 2),
+                pct_hbm_peak=round(100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                roofline_us=round(t_roof * 1e6, 2), frac_of_roofline=round(t_roof / (ms * 1e-3), 4),
+                bound="hbm" if nbytes / (HBM_PEAK_GBS * 1e9) >= flops / (MFMA_BF16_PEAK_TFLOPS * 1e12) else "mfma",
+                input_sets=SETS)
+
+
+def bench_ceiling(dev, w):
+    """What the HBM path delivers to loads alone, measured in this run (libvoxprobe.so): a grid-stride read of
+    169.6 MB regions of a 1.2 GB buffer (rotating, so the Infinity Cache cannot serve them), and the decode kernel's
+    own loads on the config-4 workload (same tiles, same per-wave load layout, same equal contiguous ranges over 256
+    workgroups, rotating over the 28 layers' planes) without its arithmetic."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from voxcpm2_arabic_dialects_turbo_amd import _lib
+
+    probe = ctypes.CDLL(os.path.join(ROOT, "voxcpm2_arabic_dialects_turbo_amd", "libvoxprobe.so"))
+    probe.vox_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
+                                            ctypes.c_void_p]
+    probe.vox_probe_tile_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                          ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    sink = torch.empty(1024, dtype=torch.uint8, device=dev)
+    stream = _lib.stream_handle(dev)
+    region = decode_bytes(w.lens) // 4096 * 4096
+    regions = 7
+    buf = torch.empty(region * regions, dtype=torch.uint8, device=dev)
+    buf.fill_(1)
+    out = {"stream_read": {}, "decode_pattern_read": {}}
+    for grid in (256, 1024, 2048):
+        def run(grid=grid):
+            for r in range(regions):
+                assert probe.vox_probe_stream_read(buf.data_ptr() + r * region, region, sink.data_ptr(), grid,
+                                                   stream) == 0
+
+        ms = _graph_ms(run, 20) / regions
+        out["stream_read"][f"grid{grid}"] = round(region / (ms * 1e-3) / 1e9, 1)
+    del buf
+    # tile offsets of the decode workload: 16-token tiles of every sequence, sequence by sequence
+    offs = []
+    for t in w.tasks:
+        for tok in range(0, t.seq_length, 16):
+            offs.append((t.block_table[tok // BS] * BS + tok % BS) * HK * D * 2)
+    tiles = torch.tensor(np.asarray(offs, dtype=np.int64), device=dev)
+    tile_bytes = len(offs) * 16 * HK * D * 2 * 2
+    for grid, depth in ((256, 1), (256, 2), (512, 1), (512, 2)):
+        def run(grid=grid, depth=depth):
+            for i, layer in enumerate(w.layers):
+                assert probe.vox_probe_tile_read(layer.k_cache.data_ptr(), layer.v_cache.data_ptr(),
+                                                 tiles.data_ptr(), len(offs), sink.data_ptr(), grid, depth,
+                                                 stream) == 0
+
+        ms = _graph_ms(run, 10) / len(w.layers)
+        out["decode_pattern_read"][f"grid{grid}_depth{depth}"] = round(tile_bytes / (ms * 1e-3) / 1e9, 1)
+    out["stream_read_best_gbs"] = max(out["stream_read"].values())
+    out["decode_pattern_read_best_gbs"] = max(out["decode_pattern_read"].values())
+    out["decode_pattern_bytes"] = tile_bytes
+    return out
+
+
 def bench_prefill(dev):
     """Benchmark config 2 prefill (packed causal varlen, production's no-prefix path) and a supplementary
     compute-bound shape; per-launch ms from graphs of launches rotating over input sets."""
@@ -365,9 +544,36 @@ def bench_kv_copy(dev):
     return out
 
 
+def cpu_config1(budget_s: float = 3.0):
+    """Benchmark config 1 on the host cores: the oracle's decode (the reference tests' fp32 _attend over the gathered
+    pages) for 1 sequence of context 512, 16 / 2 heads, fp32 caches of 4 blocks x 256 tokens in a random block order,
+    N(0, 1) inputs from seed 1; repeated for ~budget_s seconds. Bytes: the same algorithmic units as the decode
+    (fp32 elements)."""
+    import torch
+
+    from oracle import attention as ref
+
+    gen = torch.Generator().manual_seed(1)
+    table = torch.randperm(4, generator=gen).tolist()
+    kc = torch.randn(4, BS, HK, D, generator=gen)
+    vc = torch.randn(4, BS, HK, D, generator=gen)
+    q = torch.randn(1, H, D, generator=gen)
+    n, spent = 0, 0.0
+    while spent < budget_s:
+        t0 = time.perf_counter()
+        ref.decode(q, kc, vc, [512], [table], SCALE)
+        spent += time.perf_counter() - t0
+        n += 1
+    per = spent / n
+    nbytes = 512 * HK * D * 4 * 2 + H * D * 4 * 2 + 4 * (1 + 2)
+    return dict(us_per_call=round(per * 1e6, 1), gbs=round(nbytes / per / 1e9, 3), calls=n,
+                sample="BASELINE config 1: oracle decode, 1 seq x ctx 512, fp32, torch on CPU")
+
+
 def cpu_baseline(w, budget_s: float):
     """The oracle's torch path (fp32, as the reference's tests compute it) on the host cores over a bounded sample of
-    the same decode step: layer after layer (store + decode of 150 sequences) until the budget is spent."""
+    the same decode step: layer after layer (store + decode of 150 sequences) until the budget is spent; plus
+    benchmark config 1 (the reference's CPU-runnable case)."""
     import torch
 
     from oracle import attention as ref
@@ -389,7 +595,8 @@ def cpu_baseline(w, budget_s: float):
     return dict(value=round(nbytes / spent / 1e9, 3), unit="GB/s", cores=threads, kind="port",
                 sample=f"{done} of 28 layers of the config-4 decode step (store + decode, 150 sequences), "
                        f"torch fp32 on CPU, {spent:.1f} s",
-                ms_per_step_extrapolated=round(spent / done * 28 * 1e3, 1))
+                ms_per_step_extrapolated=round(spent / done * 28 * 1e3, 1),
+                config1=cpu_config1())
 
 
 TRAFFIC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
@@ -405,6 +612,11 @@ def _profiled_traffic():
     except OSError:
         return None
     return int(m.group(1)) if m else None
+
+
+def _progress(msg: str) -> None:
+    """A progress line on stderr (stdout carries only the result line)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
 def main():
@@ -467,10 +679,21 @@ def main():
             "launch_bytes": res["launch_bytes"],
         },
     }
+    _progress(f"config 4 decode: {res['ms_per_step']:.4f} ms per step, {res['launch_ms'] * 1e3:.2f} us per call")
     if not args.decode_only:
+        line["config3"] = bench_config3(dev)
+        _progress(f"config 3: {line['config3']['launch_us']} us")
+        line["config5"] = bench_config5(dev)
+        _progress(f"config 5: {line['config5']['launch_us']} us")
+        line["ceiling"] = bench_ceiling(dev, res["workload"])
+        line["roofline"]["frac_of_decode_pattern_read"] = round(
+            achieved / line["ceiling"]["decode_pattern_read_best_gbs"], 4)
+        _progress(f"ceiling: {line['ceiling']}")
         line["prefill"] = bench_prefill(dev)
+        _progress("prefill legs done")
         line["prefill"]["reference_shapes"] = bench_reference_shapes(dev)
         line["kv_block_prefix_copy"] = bench_kv_copy(dev)
+        _progress("reference shapes and kv copy done")
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(res["workload"], args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -1,7 +1,9 @@
 """Builds libvoxattn.so in-tree with hipcc for gfx950 (run as ``python -m voxcpm2_arabic_dialects_turbo_amd.build``).
 
-One shared library, C ABI only (include/vox_attn.h): no torch headers, no pybind. The sources compile in parallel
-and link into ``voxcpm2_arabic_dialects_turbo_amd/libvoxattn.so``. Packed FP32 VALU instructions are disabled for
+The attention library is one shared library, C ABI only (include/vox_attn.h): no torch headers, no pybind. The
+sources compile in parallel and link into ``voxcpm2_arabic_dialects_turbo_amd/libvoxattn.so``. Beside it,
+``libvoxprobe.so`` (include/vox_probe.h) holds the memory-rate probes bench.py runs; the attention path never loads
+it. Packed FP32 VALU instructions are disabled for
 device code (``-packed-fp32-ops``); hipcc's host pass warns that it does not know that feature, which is harmless.
 """
 
@@ -20,6 +22,8 @@ BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_NAME = "libvoxattn.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 SOURCES = ["store_kvcache.hip", "decode_attn.hip", "prefill_attn.hip", "kv_copy.hip", "capi.hip"]
+PROBE_PATH = os.path.join(PKG_DIR, "libvoxprobe.so")
+PROBE_SOURCES = ["bench_probe.hip"]
 ARCH = "gfx950"
 
 
@@ -55,23 +59,24 @@ def _run(cmd: list[str]) -> None:
 
 
 def build(verbose: bool = False) -> str:
-    """Compiles every source and links libvoxattn.so; returns its path. Always rebuilds."""
+    """Compiles every source and links libvoxattn.so and libvoxprobe.so; returns the attention library's path.
+    Always rebuilds."""
     cc = hipcc()
     os.makedirs(BUILD_DIR, exist_ok=True)
-    objs = []
     cmds = []
-    for src in SOURCES:
+    for src in SOURCES + PROBE_SOURCES:
         obj = os.path.join(BUILD_DIR, src.replace(".hip", ".o"))
-        objs.append(obj)
         cmds.append([cc, *compile_flags(), "-c", os.path.join(CSRC, src), "-o", obj])
     with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 1)) as ex:
         for cmd, fut in zip(cmds, [ex.submit(_run, c) for c in cmds]):
             if verbose:
                 print(" ".join(cmd))
             fut.result()
-    tmp = LIB_PATH + ".tmp"
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
-    os.replace(tmp, LIB_PATH)
+    for path, srcs in ((LIB_PATH, SOURCES), (PROBE_PATH, PROBE_SOURCES)):
+        objs = [os.path.join(BUILD_DIR, src.replace(".hip", ".o")) for src in srcs]
+        tmp = path + ".tmp"
+        _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
+        os.replace(tmp, path)
     return LIB_PATH
 
 

@@ -1,0 +1,101 @@
+// Memory-rate probes for bench.py (libvoxprobe.so; declared in include/vox_probe.h). They compute nothing: they
+// measure what the HBM path delivers to plain vector loads, so the decode kernel's rate can be read against the
+// ceiling of its own access pattern rather than against the datasheet alone.
+//
+//  * stream_read_kernel: one contiguous buffer, grid-stride 16-byte loads, four independent loads in flight per
+//    lane per round (the best case the memory system offers a read-only kernel).
+//  * tile_read_kernel: the decode kernel's access pattern without its arithmetic. A list of 16-token tiles (byte
+//    offsets of 16 contiguous 512-byte slot rows inside the K plane; the V tile sits at the same offset in the V
+//    plane) is cut into equal contiguous ranges, one per workgroup of 4 waves, each wave taking every fourth tile of
+//    its range. Per tile a wave issues the decode kernel's loads: K as 8 loads in MFMA A-operand layout (lane =
+//    token, 16 bytes at 64-byte steps), V as 8 coalesced loads (1 KiB per instruction). DEPTH tiles are in flight
+//    per wave (the decode kernel keeps one).
+// Every loaded word is folded into an XOR that is stored only if it hits an impossible value, so no load is dead.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "vox_common.h"
+
+namespace vox {
+namespace {
+
+constexpr int kProbeThreads = 256;
+
+__global__ __launch_bounds__(kProbeThreads) void stream_read_kernel(const u32x4* __restrict__ p, int64_t n16,
+                                                                    uint32_t* sink) {
+  const int64_t stride = (int64_t)gridDim.x * kProbeThreads;
+  int64_t i = (int64_t)blockIdx.x * kProbeThreads + threadIdx.x;
+  u32x4 acc = zero4();
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const u32x4 a = p[i], b = p[i + stride], c = p[i + 2 * stride], d = p[i + 3 * stride];
+    acc ^= a ^ b ^ c ^ d;
+  }
+  for (; i < n16; i += stride) acc ^= p[i];
+  if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x9E3779B9u && acc[0] == 0x7F4A7C15u) sink[threadIdx.x] = acc[2];
+}
+
+template <int DEPTH>
+__global__ __launch_bounds__(kProbeThreads) void tile_read_kernel(const char* __restrict__ kp,
+                                                                  const char* __restrict__ vp,
+                                                                  const int64_t* __restrict__ tiles, int64_t n,
+                                                                  uint32_t* sink) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t g = blockIdx.x, G = gridDim.x;
+  const int64_t lo = g * n / G, hi = (g + 1) * n / G;
+  const uint32_t koff = (uint32_t)((lane & 15) * 512 + (lane >> 4) * 16);
+  const uint32_t voff = (uint32_t)(lane * 16);
+  u32x4 acc = zero4();
+  u32x4 kr[DEPTH][8], vr[DEPTH][8];
+  auto issue = [&](int slot, int64_t t) {
+    const int64_t off = tiles[t];
+#pragma unroll
+    for (int kc = 0; kc < 8; ++kc) kr[slot][kc] = ld_g16(kp + off + koff + kc * 64);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vr[slot][i] = ld_g16(vp + off + voff + i * 1024);
+  };
+  int64_t t = lo + w;
+#pragma unroll
+  for (int s = 0; s < DEPTH; ++s)
+    if (t + 4 * s < hi) issue(s, t + 4 * s);
+  for (; t < hi; t += 4 * DEPTH) {
+#pragma unroll
+    for (int s = 0; s < DEPTH; ++s) {
+      const int64_t ts = t + 4 * s;
+      if (ts < hi) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc ^= kr[s][j] ^ vr[s][j];
+        if (ts + 4 * DEPTH < hi) issue(s, ts + 4 * DEPTH);
+      }
+    }
+  }
+  if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x9E3779B9u && acc[0] == 0x7F4A7C15u) sink[threadIdx.x] = acc[2];
+}
+
+}  // namespace
+}  // namespace vox
+
+extern "C" {
+
+int vox_probe_stream_read(const void* buf, int64_t bytes, void* sink, int grid, void* stream) {
+  if (!buf || !sink || bytes < 16 || grid <= 0 || ((uintptr_t)buf & 15u)) return 1;
+  vox::stream_read_kernel<<<dim3((unsigned)grid), dim3(vox::kProbeThreads), 0, (hipStream_t)stream>>>(
+      (const vox::u32x4*)buf, bytes / 16, (uint32_t*)sink);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+int vox_probe_tile_read(const void* k_plane, const void* v_plane, const int64_t* tile_offsets, int64_t n_tiles,
+                        void* sink, int grid, int depth, void* stream) {
+  if (!k_plane || !v_plane || !tile_offsets || !sink || n_tiles <= 0 || grid <= 0) return 1;
+  const dim3 g((unsigned)grid), b(vox::kProbeThreads);
+  const char* kp = (const char*)k_plane;
+  const char* vp = (const char*)v_plane;
+  if (depth == 1)
+    vox::tile_read_kernel<1><<<g, b, 0, (hipStream_t)stream>>>(kp, vp, tile_offsets, n_tiles, (uint32_t*)sink);
+  else if (depth == 2)
+    vox::tile_read_kernel<2><<<g, b, 0, (hipStream_t)stream>>>(kp, vp, tile_offsets, n_tiles, (uint32_t*)sink);
+  else
+    return 1;
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+}  // extern "C"
