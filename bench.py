@@ -327,7 +327,6 @@ def bench_ceiling(dev, w):
     probe.vox_probe_tile_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
                                           ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     sink = torch.empty(1024, dtype=torch.uint8, device=dev)
-    stream = _lib.stream_handle(dev)
     region = decode_bytes(w.lens) // 4096 * 4096
     regions = 7
     buf = torch.empty(region * regions, dtype=torch.uint8, device=dev)
@@ -337,7 +336,7 @@ def bench_ceiling(dev, w):
         def run(grid=grid):
             for r in range(regions):
                 assert probe.vox_probe_stream_read(buf.data_ptr() + r * region, region, sink.data_ptr(), grid,
-                                                   stream) == 0
+                                                   _lib.stream_handle(dev)) == 0
 
         ms = _graph_ms(run, 20) / regions
         out["stream_read"][f"grid{grid}"] = round(region / (ms * 1e-3) / 1e9, 1)
@@ -354,7 +353,7 @@ def bench_ceiling(dev, w):
             for i, layer in enumerate(w.layers):
                 assert probe.vox_probe_tile_read(layer.k_cache.data_ptr(), layer.v_cache.data_ptr(),
                                                  tiles.data_ptr(), len(offs), sink.data_ptr(), grid, depth,
-                                                 stream) == 0
+                                                 _lib.stream_handle(dev)) == 0
 
         ms = _graph_ms(run, 10) / len(w.layers)
         out["decode_pattern_read"][f"grid{grid}_depth{depth}"] = round(tile_bytes / (ms * 1e-3) / 1e9, 1)

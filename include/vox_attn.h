@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define VOX_ABI_VERSION 5
+#define VOX_ABI_VERSION 6
 
 #define VOX_OK 0
 #define VOX_EINVAL 1 /* bad argument: shape, stride, alignment or null pointer (reference: the asserts of
@@ -78,6 +78,11 @@ void vox_set_decode_workgroups(int workgroups);
  *   cu_seqlens_q/k int32 [batch + 1]; both NULL selects uniform lengths uniform_seqlen_q / uniform_seqlen_k
  *   causal         bottom-right aligned: query i of a sequence with nq queries and nk keys sees keys j <= nk-nq+i
  *   out            bf16 [T, num_heads, head_dim], token rows out_row_stride apart
+ *   workspace      NULL, or >= vox_prefill_workspace_bytes(batch) bytes of scratch: with block tables and
+ *                  cu_seqlens, sequences with exactly one query (the decode rows of a mixed prefill + decode step) then
+ *                  run on the split-KV decode kernels, which spread long contexts over every CU (needs num_heads <= 16,
+ *                  num_kv_heads 1 or 2, block_size a multiple of 32, out 16-byte aligned with out_row_stride a multiple
+ *                  of 8; otherwise, or with NULL, the prefill kernel takes every row). Same results either way.
  * Supported: head_dim 128, num_heads / num_kv_heads dividing 128. */
 int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const void* value,
                      int64_t key_row_stride, int64_t value_row_stride, const void* k_cache, const void* v_cache,
@@ -85,7 +90,11 @@ int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const
                      int max_blocks, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch,
                      int max_seqlen_q, int uniform_seqlen_q, int uniform_seqlen_k, int num_heads, int num_kv_heads,
                      int head_dim, float softmax_scale, int causal, void* out, int64_t out_row_stride,
-                     void* stream);
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Scratch bytes vox_prefill_attn's one-query rows need for `batch` sequences on the current device. No reference
+ * counterpart (flash-attn sizes its buffers internally; reference call site: nanovllm_voxcpm/model/layers.py:337). */
+size_t vox_prefill_workspace_bytes(int batch);
 
 /* vox_prefill_attn with the int8 output epilogue the W8A8 o_proj consumes. Replaces the quant=True modes of the
  * Triton paged_prefill_attention, short_causal_attention and short_attention (reference:

@@ -97,7 +97,7 @@ def test_prefill_rejects_bad_arguments():
     p = ctypes.c_void_p(256)
     # valid apart from the fake pointers: never passed unmodified (it would launch)
     args = [p, 2048, p, p, 256, 256, None, None, 0, 0, None, 0, 0, p, p, 2, 16, 0, 0, 16, 2, 128, 0.088, 1, p, 2048,
-            None]
+            None, 0, None]
     bad = list(args)
     bad[21] = 64  # head_dim
     assert lib.vox_prefill_attn(*bad) == _lib.VOX_EINVAL and "head_dim" in _err()
@@ -110,6 +110,12 @@ def test_prefill_rejects_bad_arguments():
     bad = list(args)
     bad[2] = None  # packed mode without key
     assert lib.vox_prefill_attn(*bad) == _lib.VOX_EINVAL and "key/value" in _err()
+    paged = list(args)  # paged varlen with a workspace below vox_prefill_workspace_bytes: rejected, no launch
+    paged[2:4] = [None, None]
+    paged[6:13] = [p, p, 64, 256, p, 8, 8]
+    paged[26:28] = [p, 16]
+    assert lib.vox_prefill_attn(*paged) == _lib.VOX_EINVAL and "workspace" in _err()
+    assert lib.vox_prefill_workspace_bytes(2) == lib.vox_decode_workspace_bytes(2) > 16
     zero = list(args)
     zero[15] = 0  # empty batch: nothing to do
     assert lib.vox_prefill_attn(*zero) == _lib.VOX_OK
@@ -151,7 +157,7 @@ def test_prefill_with_one_kv_head_for_128_query_heads_returns_a_status(int8):
     import sys
 
     fn = "vox_prefill_attn_int8" if int8 else "vox_prefill_attn"
-    tail = "None, p, 128 * 128, p, None" if int8 else "p, 128 * 128, None"
+    tail = "None, p, 128 * 128, p, None" if int8 else "p, 128 * 128, None, 0, None"
     code = f"""
 import ctypes, sys
 sys.path.insert(0, {os.path.dirname(os.path.dirname(os.path.abspath(__file__)))!r})

@@ -357,3 +357,29 @@ def test_paged_gather_is_bit_exact_where_a_query_sees_one_key(bs):
         v0 = vc[int(tables[b, 0]), 0]  # [HK, D]: key 0 of sequence b
         assert torch.equal(out[at], v0.repeat_interleave(H // HK, dim=0)), f"sequence {b}: query 0 != V[key 0]"
         at += n
+
+
+def test_varlen_one_query_rows_run_on_the_decode_kernels():
+    """A paged varlen call whose one-query sequences go to the split-KV decode kernels while the prefill kernel takes
+    the rest: 600 sequences (two decode launches of up to 512), mixing zero-query padding, one-query rows (one of
+    them with no keys, which gives zeros), and multi-query rows with and without a cached prefix; 64-token blocks."""
+    gen = torch.Generator().manual_seed(90)
+    nq, nk = [], []
+    for i in range(600):
+        kind = i % 6
+        q_ = [0, 1, 1, 1, 5, 37][kind]
+        k_ = 0 if kind == 0 else (q_ + int(torch.randint(0, 200, (1,), generator=gen)) if kind != 5 else q_)
+        if i == 7:
+            k_ = 0  # a one-query row with no keys
+        nq.append(q_)
+        nk.append(k_)
+    bs = 64
+    pool = sum((n + bs - 1) // bs for n in nk) + 3
+    kc, vc, tables = paged_pool(gen, nk, pool, block_size=bs)
+    q = randn(gen, sum(nq), H, D)
+    out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), _cu(nq).to(DEV), _cu(nk).to(DEV), max(nq),
+                                 max(nk), softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
+    want = ref.varlen(q.float(), _cu(nq), _cu(nk), k_cache=kc, v_cache=vc, block_tables=tables)
+    attn_close(out, want, "one-query rows on the decode kernels")
+    row7 = sum(nq[:7])
+    assert out[row7].float().abs().max().item() == 0.0, "a one-query row without keys gives zeros"

@@ -90,6 +90,37 @@ size_t vox_decode_workspace_bytes(int batch) {
   return decode_partials_bytes(slice, vox_decode_workgroups()) + ((size_t)(slice + 2) * 4 + 255) / 256 * 256;
 }
 
+}  // extern "C"
+
+namespace {
+// Launches the split and merge kernels over `batch` sequences in slices of kMaxSeqPerLaunch (each slice's step
+// layout lives in LDS), all sharing the workspace; `a` describes the whole batch.
+int launch_decode_slices(const vox::DecodeArgs& a, int batch, int num_kv_heads, void* workspace, hipStream_t stream) {
+  const int slice_max = batch < vox::kMaxSeqPerLaunch ? batch : vox::kMaxSeqPerLaunch;
+  vox::DecodeArgs base = a;
+  base.partials = (float*)workspace;
+  base.steps = (int32_t*)((char*)workspace + decode_partials_bytes(slice_max, a.grid));
+  for (int b0 = 0; b0 < batch; b0 += vox::kMaxSeqPerLaunch) {
+    vox::DecodeArgs s = base;
+    s.batch = batch - b0 < vox::kMaxSeqPerLaunch ? batch - b0 : vox::kMaxSeqPerLaunch;
+    s.block_tables = base.block_tables + (int64_t)b0 * base.bt_stride;
+    if (base.cu_q) {  // varlen: rows are absolute (cu_seqlens_q), only the sequence arrays move
+      s.cu_q = base.cu_q + b0;
+      s.cu_k = base.cu_k + b0;
+    } else {
+      s.q = base.q + (int64_t)b0 * base.q_row_stride;
+      s.context_lens = base.context_lens + b0;
+      s.out = base.out + (int64_t)b0 * base.out_row_stride;
+    }
+    const int st = hip_status(vox::launch_decode(s, num_kv_heads, stream), "decode launch");
+    if (st != VOX_OK) return st;
+  }
+  return VOX_OK;
+}
+}  // namespace
+
+extern "C" {
+
 int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
                     int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
                     int max_blocks, const int32_t* context_lens, int batch, int num_heads, int num_kv_heads,
@@ -118,9 +149,8 @@ int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, co
   const size_t need = vox_decode_workspace_bytes(batch);
   if (workspace_bytes < need || !workspace)
     return fail(VOX_EINVAL, "decode_attn: workspace of %zu bytes, %zu needed", workspace_bytes, need);
-  const int slice_max = batch < vox::kMaxSeqPerLaunch ? batch : vox::kMaxSeqPerLaunch;
 
-  vox::DecodeArgs a;
+  vox::DecodeArgs a{};
   a.q = (const uint16_t*)q;
   a.q_row_stride = q_row_stride;
   a.k_cache = (const uint16_t*)k_cache;
@@ -136,22 +166,13 @@ int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, co
   a.group = num_heads / num_kv_heads;
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   a.grid = grid;
-  a.partials = (float*)workspace;
-  a.steps = (int32_t*)((char*)workspace + decode_partials_bytes(slice_max, grid));
   a.out = (uint16_t*)out;
+  a.out_row_stride = (int64_t)num_heads * head_dim;
   // batches beyond one launch's LDS step layout run as consecutive launches on the stream (shared workspace)
-  for (int b0 = 0; b0 < batch; b0 += vox::kMaxSeqPerLaunch) {
-    vox::DecodeArgs s = a;
-    s.batch = batch - b0 < vox::kMaxSeqPerLaunch ? batch - b0 : vox::kMaxSeqPerLaunch;
-    s.q = a.q + (int64_t)b0 * q_row_stride;
-    s.block_tables = a.block_tables + (int64_t)b0 * bt_stride;
-    s.context_lens = a.context_lens + b0;
-    s.out = a.out + (int64_t)b0 * num_heads * head_dim;
-    const int st = hip_status(vox::launch_decode(s, num_kv_heads, (hipStream_t)stream), "decode_attn launch");
-    if (st != VOX_OK) return st;
-  }
-  return VOX_OK;
+  return launch_decode_slices(a, batch, num_kv_heads, workspace, (hipStream_t)stream);
 }
+
+size_t vox_prefill_workspace_bytes(int batch) { return vox_decode_workspace_bytes(batch); }
 
 }  // extern "C"
 
@@ -227,7 +248,7 @@ int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const
                      int max_blocks, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch,
                      int max_seqlen_q, int uniform_seqlen_q, int uniform_seqlen_k, int num_heads, int num_kv_heads,
                      int head_dim, float softmax_scale, int causal, void* out, int64_t out_row_stride,
-                     void* stream) {
+                     void* workspace, size_t workspace_bytes, void* stream) {
   if (batch < 0 || max_seqlen_q < 0) return fail(VOX_EINVAL, "prefill_attn: negative batch or max_seqlen_q");
   if (batch == 0 || max_seqlen_q == 0) return VOX_OK;
   if (!out) return fail(VOX_EINVAL, "prefill_attn: null out");
@@ -241,7 +262,45 @@ int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const
   if (st != VOX_OK) return st;
   a.out = (uint16_t*)out;
   a.out_row_stride = out_row_stride;
-  return hip_status(vox::launch_prefill(a, max_seqlen_q, (hipStream_t)stream), "prefill_attn launch");
+  const hipStream_t s = (hipStream_t)stream;
+  // One-query sequences of a paged varlen call (the decode rows of a mixed step) go to the split-KV decode kernels,
+  // which spread long contexts over every CU; the prefill kernel takes the rest. Needs the workspace and the decode
+  // kernels' shapes; otherwise the prefill kernel takes every row.
+  const bool decode_rows = workspace && block_tables && cu_seqlens_q && num_heads <= kMaxHeads &&
+                           (num_kv_heads == 1 || num_kv_heads == 2) && block_size % 32 == 0 &&
+                           (int64_t)max_blocks * block_size <= (1 << 30) && out_row_stride % 8 == 0 &&
+                           ((uintptr_t)out & 15u) == 0;
+  if (decode_rows) {
+    const size_t need = vox_prefill_workspace_bytes(batch);
+    if (workspace_bytes < need)
+      return fail(VOX_EINVAL, "prefill_attn: workspace of %zu bytes, %zu needed", workspace_bytes, need);
+    a.skip_single = 1;
+    if (max_seqlen_q > 1) {
+      const int sp = hip_status(vox::launch_prefill(a, max_seqlen_q, s), "prefill_attn launch");
+      if (sp != VOX_OK) return sp;
+    }
+    vox::DecodeArgs d{};
+    d.q = a.q;
+    d.q_row_stride = q_row_stride;
+    d.k_cache = a.k_cache;
+    d.v_cache = a.v_cache;
+    d.num_blocks = num_blocks;
+    d.block_size = block_size;
+    d.block_tables = block_tables;
+    d.bt_stride = bt_stride;
+    d.max_blocks = max_blocks;
+    d.batch = batch;
+    d.num_heads = num_heads;
+    d.group = num_heads / num_kv_heads;
+    d.scale_log2 = a.scale_log2;
+    d.grid = vox_decode_workgroups();
+    d.out = a.out;
+    d.out_row_stride = out_row_stride;
+    d.cu_q = cu_seqlens_q;
+    d.cu_k = cu_seqlens_k;
+    return launch_decode_slices(d, batch, num_kv_heads, workspace, s);
+  }
+  return hip_status(vox::launch_prefill(a, max_seqlen_q, s), "prefill_attn launch");
 }
 
 int vox_prefill_attn_int8(const void* q, int64_t q_row_stride, const void* key, const void* value,

@@ -3,7 +3,10 @@
 // Semantics (reference call: nanovllm_voxcpm/model/layers.py:350-358, flash_attn_with_kvcache with cache_seqlens and
 // block_table, causal, softmax_scale): for every sequence b and query head h,
 //   o[b, h] = softmax_j(scale * q[b, h] . K[b, j, h // G]) V[b, j, h // G],   j < context_lens[b],
-// where token j lives in cache block block_tables[b, j // block_size] at slot j % block_size, G = H / HK.
+// where token j lives in cache block block_tables[b, j // block_size] at slot j % block_size, G = H / HK. The same
+// kernels also serve the one-query rows of a paged varlen call (the decode rows of a mixed prefill + decode step,
+// reference: nanovllm_voxcpm/model/layers.py:337-348 with block_table): there a sequence's context is its key count
+// when it has exactly one query, and its q / output row is cu_seqlens_q[b].
 //
 // gfx950 mapping.
 //  * Work split (persistent, balanced): the tokens of all sequences are cut into 64-token steps, laid end to end in
@@ -122,6 +125,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   constexpr int kLdsBytes = (kVtElems * 2 > kRedFloats * 4) ? kVtElems * 2 : kRedFloats * 4;
   __shared__ __attribute__((aligned(16))) unsigned char lds_raw[kLdsBytes];
   __shared__ int s_ctx[kMaxSeqPerLaunch];        // context per sequence, cut to the table's reach
+  __shared__ int s_row[kMaxSeqPerLaunch];        // q / output row per sequence
   __shared__ int s_start[kMaxSeqPerLaunch + 1];  // first step per sequence; s_start[batch] = total steps
   __shared__ int s_wtot[kWaves];
   __shared__ int s_wmax[kWaves];  // most steps of one sequence, per wave
@@ -140,7 +144,19 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   // the first kThreads sequences and every table entry a thread stages are loaded before any of them is waited for:
   // one round trip (a load-then-store loop waits for each load in turn, one round trip per kThreads entries).
   const int mb = p.max_blocks;
-  const int ctx_first = tid < p.batch ? p.context_lens[tid] : 0;
+  const bool varlen = p.cu_q != nullptr;
+  // sequence bb's context and row: context_lens[bb] and bb, or in varlen mode its key count when it has one query
+  auto seq_of = [&](int bb, int& row) -> int {
+    if (!varlen) {
+      row = bb;
+      return p.context_lens[bb];
+    }
+    const int q0 = p.cu_q[bb], q1 = p.cu_q[bb + 1], k0 = p.cu_k[bb], k1 = p.cu_k[bb + 1];
+    row = q0;
+    return q1 - q0 == 1 ? k1 - k0 : 0;
+  };
+  int row_first = 0;
+  const int ctx_first = tid < p.batch ? seq_of(tid, row_first) : 0;
   if constexpr (BTL) {
     constexpr int kPer = (kBtLds + kThreads - 1) / kThreads;  // entries per thread at most
     const int nbt = p.batch * mb;
@@ -167,7 +183,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   int nmax = 0;  // most steps of one sequence
   for (int base = 0; base < p.batch; base += kThreads) {
     const int bb = base + tid;
-    const int raw = base == 0 ? ctx_first : (bb < p.batch ? p.context_lens[bb] : 0);
+    int row = row_first;
+    const int raw = base == 0 ? ctx_first : (bb < p.batch ? seq_of(bb, row) : 0);
     const int ctx = bb < p.batch ? max(0, min(raw, max_ctx)) : 0;
     const int n = (ctx + kStep - 1) / kStep;
     const int incl = wave_incl_scan(n, lane);
@@ -188,6 +205,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
     }
     if (bb < p.batch) {
       s_ctx[bb] = ctx;
+      s_row[bb] = row;
       s_start[bb] = run + before + incl - n;
     }
     run += total;
@@ -227,6 +245,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
 
   while (r < r1) {
     const int ctx = uniform(s_ctx[b]);
+    const int64_t row = uniform(s_row[b]);
     const int sb = uniform(s_start[b]);
     const int nb = uniform(s_start[b + 1]) - sb;
     if (nb == 0) {  // an empty row holds no step
@@ -271,7 +290,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
     if (first < tok_end) {
       u32x4 qv[4];
       {
-        const uint16_t* qb = p.q + (int64_t)b * p.q_row_stride + (int64_t)(h < H ? h : 0) * kD + jq * 8;
+        const uint16_t* qb = p.q + row * p.q_row_stride + (int64_t)(h < H ? h : 0) * kD + jq * 8;
 #pragma unroll
         for (int kq = 0; kq < 4; ++kq) qv[kq] = ld_g16(qb + kq * 32);
       }
@@ -398,7 +417,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
         const float inv = L > 0.f ? 1.f / L : 0.f;
 #pragma unroll
         for (int i = 0; i < kDpt / 4; ++i)
-          *reinterpret_cast<u32x2*>(p.out + ((int64_t)b * H + hh) * kD + d0 + 4 * i) =
+          *reinterpret_cast<u32x2*>(p.out + row * p.out_row_stride + (int64_t)hh * kD + d0 + 4 * i) =
               u32x2{pack_bf16x2(o[i][0] * inv, o[i][1] * inv), pack_bf16x2(o[i][2] * inv, o[i][3] * inv)};
       }
     } else {  // cut by a range boundary: partial for decode_merge_kernel, slot b + g
@@ -417,8 +436,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   }
 }
 
-// Writes the sequences that decode_kernel left as partials, and the zeros of empty rows. One workgroup per
-// sequence, thread = (head, 8 dims). Sequence b covers steps [sb, eb) of the layout decode_kernel published in
+// Writes the sequences that decode_kernel left as partials, and the zeros of empty rows (in varlen mode only those of
+// one-query sequences; the others belong to the prefill kernel). One workgroup per sequence, thread = (head, 8 dims). Sequence b covers steps [sb, eb) of the layout decode_kernel published in
 // `steps`, with the number G of workgroups it used; workgroup g of G covers [floor(g S / G), floor((g + 1) S / G))
 // (at least one step, as G <= S), and the workgroups touching b, g_first..g_last below, each left a partial at slot
 // b + g. Online rescale over the partials (fp32), the loads of kMergeBatch partials in flight together. Runs after
@@ -433,7 +452,12 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs p) {
   const int64_t sb = p.steps[b];
   const int64_t eb = p.steps[b + 1];
   const int64_t G = p.steps[p.batch + 1];  // active workgroups (with S >= 1, none has an empty range)
-  uint16_t* ob = p.out + ((int64_t)b * H + hh) * kD + d0;
+  int64_t row = b;
+  if (p.cu_q) {
+    row = p.cu_q[b];
+    if (p.cu_q[b + 1] - row != 1) return;  // not a one-query row: the prefill kernel writes it
+  }
+  uint16_t* ob = p.out + row * p.out_row_stride + (int64_t)hh * kD + d0;
   if (hh >= H) return;
   if (eb == sb) {  // empty (padded) row: defined zeros
     *reinterpret_cast<u32x4*>(ob) = zero4();

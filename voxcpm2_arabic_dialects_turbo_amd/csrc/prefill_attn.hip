@@ -117,7 +117,7 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
   if (KV != kPacked) nk = min(nk, p.max_blocks * p.block_size);  // keys the block table can address
   const int G = p.group;
   const int BQ = ROWS / G;  // query tokens per workgroup
-  if (qt * BQ >= nq) return;
+  if (qt * BQ >= nq || (p.skip_single && nq == 1)) return;  // (one-query rows: the decode kernel's, in varlen mode)
 
   const int tid = threadIdx.x & (NT - 1);  // thread within the half
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform

@@ -31,7 +31,13 @@ struct DecodeArgs {
   int grid;                   // workgroups of the split kernel (persistent, balanced ranges)
   float* partials;            // [B + grid, kPartialFloats]
   int32_t* steps;             // [B + 2]: first 64-token step of every sequence, the total, the active workgroups
-  uint16_t* out;              // bf16 [B, H, 128], contiguous
+  uint16_t* out;              // bf16 [B, H, 128]: sequence rows out_row_stride apart, heads 128 apart
+  int64_t out_row_stride;
+  // Varlen mode (cu_q != nullptr; context_lens unused): the one-query rows of a varlen call. Sequence b is handled
+  // when it has exactly one query (cu_q[b + 1] - cu_q[b] == 1): its keys are the first cu_k[b + 1] - cu_k[b] tokens
+  // of its table row, and its q and output row is cu_q[b]. Every other sequence is left alone: no keys, no output.
+  const int32_t* cu_q;
+  const int32_t* cu_k;
 };
 
 struct PrefillArgs {
@@ -69,6 +75,7 @@ struct PrefillArgs {
   int8_t* out_q;              // int8 [T, H * 128]; token rows out_row_stride apart
   float* out_scale;           // fp32 [T]
   int xcd_order;              // set by the launcher: run contiguous (q tile, sequence, kv head) ranges per XCD
+  int skip_single;            // sequences with exactly one query are left to the decode kernel (varlen mode)
 };
 
 struct CopyArgs {

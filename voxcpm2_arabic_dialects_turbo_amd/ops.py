@@ -207,11 +207,17 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor | None, v: torch.Tensor | 
                                              _lib.stream_handle(dev)),
                    "prefill_attn_int8")
         return out
+    # paged varlen: one-query rows (decode rows of a mixed step) run on the split-KV decode kernels, which need scratch
+    ws = None
+    if block_table is not None and cu_q is not None:
+        ws = torch.empty(max(lib.vox_prefill_workspace_bytes(B), 16), dtype=torch.uint8, device=dev)
     _lib.check(lib.vox_prefill_attn(q.data_ptr(), q.stride(0), *args,
                                     None if cu_q is None else cu_q.data_ptr(),
                                     None if cu_k is None else cu_k.data_ptr(), B, int(max_seqlen_q),
                                     int(uniform_seqlen_q), int(uniform_seqlen_k), H, HK, D, float(softmax_scale),
-                                    1 if causal else 0, out.data_ptr(), out.stride(0), _lib.stream_handle(dev)),
+                                    1 if causal else 0, out.data_ptr(), out.stride(0),
+                                    None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
+                                    _lib.stream_handle(dev)),
                "prefill_attn")
     return out
 
