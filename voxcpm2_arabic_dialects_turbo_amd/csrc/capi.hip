@@ -275,6 +275,7 @@ int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const
     if (workspace_bytes < need)
       return fail(VOX_EINVAL, "prefill_attn: workspace of %zu bytes, %zu needed", workspace_bytes, need);
     a.skip_single = 1;
+    a.persistent = 1;  // the (q tile, sequence) grid would be mostly the decode rows' empty tiles
     if (max_seqlen_q > 1) {
       const int sp = hip_status(vox::launch_prefill(a, max_seqlen_q, s), "prefill_attn launch");
       if (sp != VOX_OK) return sp;

@@ -105,15 +105,6 @@ __device__ __forceinline__ int active_workgroups(int grid, int64_t steps, int ma
 // A value every lane of the wave holds, moved to a scalar register (LDS reads land in vector registers).
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
-__device__ __forceinline__ int wave_incl_scan(int x, int lane) {
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const int y = __shfl_up(x, o, kWave);
-    if (lane >= o) x += y;
-  }
-  return x;
-}
-
 template <int HK, bool BTL>
 __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   using TT = Tile<HK>;

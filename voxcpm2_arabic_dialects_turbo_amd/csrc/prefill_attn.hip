@@ -60,8 +60,9 @@ enum KvSource { kPacked = 0, kPagedTiles = 1, kPagedPieces = 2 };
 // NW waves per KV group, each owning RT 16-row blocks of the 128 query rows: 4 waves x 32 rows keep the LDS reads per
 // MFMA low (the largest grids); 8 waves x 16 rows halve each wave's work per key tile, which shortens a workgroup's
 // chain of key tiles (smaller grids, where the longest chains end the launch).
+// One work item: query tile qt of sequence b, kv head gz (QUANT: every kv head, one per half of the workgroup).
 template <bool QUANT, int KV, int NW, int RT>
-__global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 : 2) void prefill_kernel(PrefillArgs p) {
+__device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b, int gz) {
   constexpr int NH = QUANT ? 2 : 1;  // KV-group halves per workgroup
   constexpr int ROWS = 16 * RT * NW;  // query rows per KV group
   constexpr int NT = 64 * NW;        // threads per KV group
@@ -73,22 +74,6 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
   // per-piece path: whether each key of the staged tile lies in a mapped block (an unmapped block's keys are masked)
   __shared__ __attribute__((aligned(16))) unsigned char s_keyok[NH][KV == kPagedPieces ? kBK : 4];
 
-  // Work item (q tile, sequence, kv head). Workgroup i runs on XCD i % 8; with xcd_order each XCD gets a contiguous
-  // run of work items, so the query tiles that re-read a sequence's K/V tiles find them in that XCD's L2 (the
-  // launcher sets it for large grids; on small ones the runs would hold uneven numbers of empty tiles). A causal
-  // run starts at each sequence's last query tile, the one with the most key tiles, so the light tiles fill the end
-  // of the run instead of the heavy ones (16 x 2048 tokens -3 %, 2 x 8192 -5 %).
-  int qt = blockIdx.x, b = blockIdx.y, gz = blockIdx.z;
-  if (p.xcd_order) {
-    const unsigned nwg = gridDim.x * gridDim.y * gridDim.z;
-    const unsigned id = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-    const unsigned xq = nwg / kXcds, xr = nwg % kXcds, xcd = id % kXcds, loc = id / kXcds;
-    const unsigned work = (xcd < xr ? xcd * (xq + 1) : xr * (xq + 1) + (xcd - xr) * xq) + loc;
-    qt = (int)(work % gridDim.x);
-    b = (int)((work / gridDim.x) % gridDim.y);
-    gz = (int)(work / (gridDim.x * gridDim.y));
-    if (p.causal) qt = (int)gridDim.x - 1 - qt;  // heavy query tiles first
-  }
   const int half = QUANT ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x / NT)) : 0;  // wave-uniform
   const int g = QUANT ? half : gz;
   auto& ks = ks_all[half];
@@ -637,6 +622,78 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
   }
 }
 
+// Grid forms. Non-persistent: one workgroup per (q tile, sequence, kv head) of the grid. Workgroup i runs on XCD
+// i % 8; with xcd_order each XCD gets a contiguous run of work items, so the query tiles that re-read a sequence's
+// K/V tiles find them in that XCD's L2 (the launcher sets it for large grids; on small ones the runs would hold
+// uneven numbers of empty tiles). A causal run starts at each sequence's last query tile, the one with the most key
+// tiles, so the light tiles fill the end of the run instead of the heavy ones (16 x 2048 tokens -3 %, 2 x 8192 -5 %).
+// Persistent (PER): a fixed grid, for calls whose (q tile, sequence) grid would be mostly empty (a mixed step's
+// decode rows, left to the decode kernel): each workgroup scans cu_q once, numbers the items of the sequences that
+// have work (heaviest causal q tile first within a sequence, both kv heads of a tile together), and takes every
+// gridDim.x-th item from its own index on. An empty workgroup of the plain grid costs a memory round trip to find
+// it has nothing to do; a grid of a few thousand of them took longer than the work itself.
+template <bool QUANT, int KV, int NW, int RT, bool PER>
+__global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 : 2) void prefill_kernel(PrefillArgs p) {
+  if constexpr (PER) {
+    constexpr int NTH = 64 * NW * (QUANT ? 2 : 1);
+    constexpr int ROWS = 16 * RT * NW;
+    __shared__ int s_first[kMaxSeqPerLaunch + 1];  // first item of each sequence; s_first[batch] = the total
+    __shared__ int s_wtot[NTH / 64];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int BQ = ROWS / p.group;
+    const int HKz = QUANT ? 1 : p.num_kv_heads;
+    int run = 0;
+    for (int base = 0; base < p.batch; base += NTH) {
+      const int bb = base + tid;
+      int n = 0;
+      if (bb < p.batch) {
+        const int nq = max(p.cu_q[bb + 1] - p.cu_q[bb], 0);
+        n = (p.skip_single && nq == 1) ? 0 : (nq + BQ - 1) / BQ * HKz;
+      }
+      const int incl = wave_incl_scan(n, lane);
+      if (lane == kWave - 1) s_wtot[w] = incl;
+      __syncthreads();
+      int before = 0, total = 0;
+#pragma unroll
+      for (int ww = 0; ww < NTH / 64; ++ww) {
+        before += ww < w ? s_wtot[ww] : 0;
+        total += s_wtot[ww];
+      }
+      if (bb < p.batch) s_first[bb] = run + before + incl - n;
+      run += total;
+      __syncthreads();
+    }
+    if (tid == 0) s_first[p.batch] = run;
+    __syncthreads();
+    for (int i = blockIdx.x; i < run; i += gridDim.x) {
+      int lo = 0, hi = p.batch;  // the last b with s_first[b] <= i (an empty sequence shares the next one's start)
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (__builtin_amdgcn_readfirstlane(s_first[mid]) <= i) lo = mid; else hi = mid;
+      }
+      const int first = __builtin_amdgcn_readfirstlane(s_first[lo]);
+      const int nt = (__builtin_amdgcn_readfirstlane(s_first[lo + 1]) - first) / HKz;
+      const int local = i - first;
+      const int r = local / HKz;
+      prefill_tile<QUANT, KV, NW, RT>(p, p.causal ? nt - 1 - r : r, lo, local % HKz);
+      __syncthreads();  // the item's LDS is free for the next one
+    }
+  } else {
+    int qt = blockIdx.x, b = blockIdx.y, gz = blockIdx.z;
+    if (p.xcd_order) {
+      const unsigned nwg = gridDim.x * gridDim.y * gridDim.z;
+      const unsigned id = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+      const unsigned xq = nwg / kXcds, xr = nwg % kXcds, xcd = id % kXcds, loc = id / kXcds;
+      const unsigned work = (xcd < xr ? xcd * (xq + 1) : xr * (xq + 1) + (xcd - xr) * xq) + loc;
+      qt = (int)(work % gridDim.x);
+      b = (int)((work / gridDim.x) % gridDim.y);
+      gz = (int)(work / (gridDim.x * gridDim.y));
+      if (p.causal) qt = (int)gridDim.x - 1 - qt;  // heavy query tiles first
+    }
+    prefill_tile<QUANT, KV, NW, RT>(p, qt, b, gz);
+  }
+}
+
 }  // namespace
 
 static int device_cus() {
@@ -649,21 +706,39 @@ static int device_cus() {
   return cus;
 }
 
-template <bool QUANT, int NW, int RT>
+template <bool QUANT, int NW, int RT, bool PER = false>
 hipError_t launch_prefill_kind(const PrefillArgs& a, dim3 grid, hipStream_t stream) {
   const dim3 block(64 * NW * (QUANT ? a.num_kv_heads : 1));
   if (!a.block_tables)
-    prefill_kernel<QUANT, kPacked, NW, RT><<<grid, block, 0, stream>>>(a);
+    prefill_kernel<QUANT, kPacked, NW, RT, PER><<<grid, block, 0, stream>>>(a);
   else if (a.block_size % kBK == 0)
-    prefill_kernel<QUANT, kPagedTiles, NW, RT><<<grid, block, 0, stream>>>(a);
+    prefill_kernel<QUANT, kPagedTiles, NW, RT, PER><<<grid, block, 0, stream>>>(a);
   else
-    prefill_kernel<QUANT, kPagedPieces, NW, RT><<<grid, block, 0, stream>>>(a);
+    prefill_kernel<QUANT, kPagedPieces, NW, RT, PER><<<grid, block, 0, stream>>>(a);
   return hipGetLastError();
 }
 
 hipError_t launch_prefill(const PrefillArgs& a0, int max_seqlen_q, hipStream_t stream) {
   if (max_seqlen_q <= 0 || a0.batch <= 0) return hipSuccess;
   PrefillArgs a = a0;
+  if (a.persistent) {
+    // 4 waves of 16 rows (64 / G tokens per item; the shorter key-tile chain per item), two workgroups per CU, at
+    // most one workgroup per item; sequences in slices of kMaxSeqPerLaunch (rows stay absolute through cu_q)
+    if (!a.cu_q || 64 % a.group) return hipErrorInvalidValue;
+    const int64_t bq = 64 / a.group;
+    for (int b0 = 0; b0 < a0.batch; b0 += kMaxSeqPerLaunch) {
+      PrefillArgs s = a;
+      s.batch = a0.batch - b0 < kMaxSeqPerLaunch ? a0.batch - b0 : kMaxSeqPerLaunch;
+      s.cu_q = a.cu_q + b0;
+      s.cu_k = a.cu_k + b0;
+      if (s.block_tables) s.block_tables = a.block_tables + (int64_t)b0 * a.bt_stride;
+      const int64_t items = ((int64_t)max_seqlen_q + bq - 1) / bq * s.batch * s.num_kv_heads;
+      const int64_t grid = items < 2 * device_cus() ? items : 2 * device_cus();
+      const hipError_t e = launch_prefill_kind<false, 4, 1, true>(s, dim3((unsigned)grid), stream);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
   // 4 waves of 16 rows (64 / G tokens per workgroup) when that grid fits two workgroups per CU at once: rows that
   // hold no query token still run every key tile, and a 128-row workgroup over a few tokens is mostly such rows
   // (measured: head-start step 200 x 7 tokens 7.4 -> 6.8 us, LocEnc 150 x 5 6.1 -> 5.5 us). Up to four per CU when

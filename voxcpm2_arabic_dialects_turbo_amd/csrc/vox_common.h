@@ -71,6 +71,16 @@ __device__ __forceinline__ float col_sum4(float x) { return xrow_sum(xhalf_sum(x
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Inclusive prefix sum over the 64 lanes of a wavefront.
+__device__ __forceinline__ int wave_incl_scan(int x, int lane) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int y = __shfl_up(x, o, kWave);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
 // s_waitcnt vmcnt(0): every vector memory load of this wave has landed. Placed after loads whose registers stay live
 // across a software-pipelined loop (the query operands), it lets the compiler's wait analysis see them as complete
 // at the loop header; otherwise it falls back to a full vmcnt(0) inside the loop, which also waits for the

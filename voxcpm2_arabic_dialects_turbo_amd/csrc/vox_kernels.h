@@ -76,6 +76,8 @@ struct PrefillArgs {
   float* out_scale;           // fp32 [T]
   int xcd_order;              // set by the launcher: run contiguous (q tile, sequence, kv head) ranges per XCD
   int skip_single;            // sequences with exactly one query are left to the decode kernel (varlen mode)
+  int persistent;             // set by the launcher: a fixed grid loops over the (q tile, kv head) items of the
+                              // sequences, found by a scan of cu_q (at most kMaxSeqPerLaunch sequences per launch)
 };
 
 struct CopyArgs {
