@@ -383,3 +383,34 @@ def test_varlen_one_query_rows_run_on_the_decode_kernels():
     attn_close(out, want, "one-query rows on the decode kernels")
     row7 = sum(nq[:7])
     assert out[row7].float().abs().max().item() == 0.0, "a one-query row without keys gives zeros"
+
+
+def test_mixed_step_captured_in_a_hip_graph_replays_like_eager():
+    """A mixed prefill + decode varlen call runs its decode rows on the caller's stream and its prefill rows on the
+    library's second stream (event fork and join). Captured in a HIP graph and replayed four times, with eager calls on
+    other inputs between the replays, every replay equals the eager result bit for bit, which is within tolerance of
+    the oracle."""
+    gen = torch.Generator().manual_seed(91)
+    pre, dec = [300, 450, 77], [700, 130, 1500, 2, 999]
+    nk, nq = pre + dec, pre + [1] * len(dec)
+    kc, vc, tables = paged_pool(gen, nk, 40)
+    q = randn(gen, sum(nq), H, D)
+    q2 = randn(gen, sum(nq), H, D)
+    d = dict(k=kc.to(DEV), v=vc.to(DEV), cu_seqlens_q=_cu(nq).to(DEV), cu_seqlens_k=_cu(nk).to(DEV),
+             max_seqlen_q=max(nq), max_seqlen_k=max(nk), softmax_scale=SCALE, causal=True,
+             block_table=tables.to(DEV))
+    q_d, q2_d = q.to(DEV), q2.to(DEV)
+    eager = flash_attn_varlen_func(q_d, **d)
+    eager2 = flash_attn_varlen_func(q2_d, **d)
+    torch.cuda.synchronize()
+    attn_close(eager, ref.varlen(q.float(), _cu(nq), _cu(nk), k_cache=kc, v_cache=vc, block_tables=tables), "eager")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        static = flash_attn_varlen_func(q_d, **d)
+    for r in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static, eager), f"replay {r} differs from the eager call"
+        other = flash_attn_varlen_func(q2_d, **d)
+        torch.cuda.synchronize()
+        assert torch.equal(other, eager2)
