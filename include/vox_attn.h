@@ -57,6 +57,19 @@ int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, co
                     int head_dim, float softmax_scale, void* workspace, size_t workspace_bytes, void* out,
                     void* stream);
 
+/* vox_decode_attn without the workspace argument: the split-KV scratch is a static device array of 16 MiB
+ * (16777216 bytes) that each GPU the library runs on holds until the process ends, so the
+ * call allocates nothing (no hipMalloc, no allocator call of any kind). No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture that must not touch an allocator, tight serving loops).
+ * Returns VOX_EINVAL when vox_decode_workspace_bytes(batch) exceeds the array (not for any batch at the default
+ * workgroup count: batches are launched 512 sequences at a time). Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (different streams, or host threads) race and must be serialized by the caller.
+ * The array needs no clearing: each call writes every scratch value it reads. Other arguments as vox_decode_attn. */
+int vox_decode_attn_noalloc(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
+                            int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
+                            int max_blocks, const int32_t* context_lens, int batch, int num_heads, int num_kv_heads,
+                            int head_dim, float softmax_scale, void* out, void* stream);
+
 /* Scratch bytes vox_decode_attn needs for `batch` sequences on the current device (split-KV partials). No reference
  * counterpart: flash-attn sizes its split-KV buffers internally (reference call site: nanovllm_voxcpm/model/layers.py:350). */
 size_t vox_decode_workspace_bytes(int batch);

@@ -25,6 +25,7 @@ EXPORTS = (
     "vox_abi_version",
     "vox_store_kvcache",
     "vox_decode_attn",
+    "vox_decode_attn_noalloc",
     "vox_decode_workspace_bytes",
     "vox_decode_workgroups",
     "vox_set_decode_workgroups",
@@ -43,6 +44,8 @@ _SIGNATURES = {
                                  _i32, _i32, _c_void_p]),
     "vox_decode_attn": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _i64, _i32,
                                _c_void_p, _i32, _i32, _i32, _i32, _f32, _c_void_p, _size, _c_void_p, _c_void_p]),
+    "vox_decode_attn_noalloc": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _i64, _i32,
+                                       _c_void_p, _i32, _i32, _i32, _i32, _f32, _c_void_p, _c_void_p]),
     "vox_decode_workspace_bytes": (_size, [_i32]),
     "vox_decode_workgroups": (_i32, []),
     "vox_set_decode_workgroups": (None, [_i32]),

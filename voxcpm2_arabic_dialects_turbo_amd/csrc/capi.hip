@@ -220,6 +220,63 @@ size_t vox_prefill_workspace_bytes(int batch) { return vox_decode_workspace_byte
 
 }  // extern "C"
 
+// ---- allocation-free decode: the split-KV scratch in a static device array ----------------------------------------
+//
+// vox_decode_attn_noalloc serves callers that cannot allocate (code under HIP graph capture that must not touch an
+// allocator, tight serving loops): the workspace vox_decode_attn takes as an argument lives in `scratch`, a
+// file-scope device array that every GPU the library runs on holds until the process ends. In host code `scratch`
+// names a host-side stand-in, not the device array: its device address on each GPU comes from hipGetSymbolAddress,
+// looked up once per device with that device current, and only that address is handed to kernels.
+namespace {
+constexpr size_t kScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+void* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+// This device's address of `scratch` (nullptr and an error message on failure).
+void* scratch_on_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    fail(VOX_EHIP, "decode_attn_noalloc: no current device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      (void)hipGetLastError();
+      fail(VOX_EHIP, "decode_attn_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" {
+
+int vox_decode_attn_noalloc(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
+                            int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
+                            int max_blocks, const int32_t* context_lens, int batch, int num_heads, int num_kv_heads,
+                            int head_dim, float softmax_scale, void* out, void* stream) {
+  if (batch < 0) return fail(VOX_EINVAL, "decode_attn_noalloc: batch < 0");
+  if (batch == 0) return VOX_OK;
+  const size_t need = vox_decode_workspace_bytes(batch);
+  if (need > kScratchBytes)
+    return fail(VOX_EINVAL, "decode_attn_noalloc: needs %zu bytes of scratch, the static array holds %zu", need,
+                kScratchBytes);
+  void* ws = scratch_on_current_device();
+  if (!ws) return VOX_EHIP;
+  return vox_decode_attn(q, q_row_stride, k_cache, v_cache, num_blocks, block_size, block_tables, bt_stride,
+                         max_blocks, context_lens, batch, num_heads, num_kv_heads, head_dim, softmax_scale, ws,
+                         kScratchBytes, out, stream);
+}
+
+}  // extern "C"
+
 namespace {
 // Validates a prefill call's shared arguments (all but the output) and fills its launch descriptor.
 int prefill_setup(const char* fn, const void* q, int64_t q_row_stride, const void* key, const void* value,
