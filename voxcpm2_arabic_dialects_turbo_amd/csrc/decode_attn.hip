@@ -9,7 +9,7 @@
 // when it has exactly one query, and its q / output row is cu_seqlens_q[b].
 //
 // gfx950 mapping.
-//  * Work split (persistent, balanced): the tokens of all sequences are cut into 64-token steps, laid end to end in
+//  * Work split (persistent, balanced): the tokens of all sequences are cut into 16-token steps, laid end to end in
 //    sequence order, and a fixed grid of workgroups (one per CU by default) takes equal contiguous ranges of steps.
 //    Every workgroup streams the same number of bytes; it walks its range sequence by sequence. The step layout
 //    comes from a scan of context_lens inside the kernel, so the launch shape depends only on host-known sizes
@@ -40,7 +40,9 @@ constexpr int kD = 128;
 constexpr int kTile = 16;              // tokens per wave iteration
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * kWave;
-constexpr int kStep = kWaves * kTile;  // tokens per workgroup step
+constexpr int kStep = kWaves * kTile;  // tokens per workgroup step (the 4 waves' tiles side by side)
+// The work is balanced in units of one wave tile: with 64-token units a config-4 launch (2700 units over 256
+// workgroups) gave some workgroups 11 units and others 10, and the 11-unit ones (10 % more bytes) ended the launch.
 constexpr int kMaxHeads = 16;
 #ifndef VOX_MAX_PIECES
 #define VOX_MAX_PIECES 32
@@ -105,16 +107,22 @@ __device__ __forceinline__ int active_workgroups(int grid, int64_t steps, int ma
 // A value every lane of the wave holds, moved to a scalar register (LDS reads land in vector registers).
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// A workgroup's range is worked in rounds of up to kRoundSegs segments (a segment = the part of one sequence inside
+// the range). In a round each wave takes an equal contiguous share of the round's tiles, across segment boundaries,
+// and leaves one fp32 partial per segment it touched in LDS; one barrier, then the workgroup merges the round's
+// segments. Wave w's share follows wave w - 1's, so the (wave, segment) pairs of a round form a staircase and
+// pair (w, k) can use slot w + k. (With the waves taking a segment's tiles in turn instead, every segment ended in a
+// barrier at which the waves with one tile fewer than the others waited a whole tile round trip: ~2 us per segment.)
+constexpr int kRoundSegs = 8;
+constexpr int kSlots = kRoundSegs + kWaves - 1;
+
 template <int HK, bool BTL>
 __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   using TT = Tile<HK>;
   constexpr int ROW = TT::ROW;
   constexpr int VROW = ROW + 16;  // padded LDS row: the 16 rows a transposed read touches hit distinct banks
-  // Per-wave V tiles [16 tokens][VROW]; reused as fp32 scratch for the in-workgroup merge.
-  constexpr int kVtElems = kWaves * kTile * VROW;
-  constexpr int kRedFloats = kWaves * kMaxHeads * kD + 2 * kWaves * kMaxHeads;
-  constexpr int kLdsBytes = (kVtElems * 2 > kRedFloats * 4) ? kVtElems * 2 : kRedFloats * 4;
-  __shared__ __attribute__((aligned(16))) unsigned char lds_raw[kLdsBytes];
+  __shared__ __attribute__((aligned(16))) uint16_t s_vt[kWaves * kTile * VROW];  // per-wave V tiles [16][VROW]
+  __shared__ __attribute__((aligned(16))) float s_slot[kSlots * kPartialFloats];  // (wave, segment) partials
   __shared__ int s_ctx[kMaxSeqPerLaunch];        // context per sequence, cut to the table's reach
   __shared__ int s_row[kMaxSeqPerLaunch];        // q / output row per sequence
   __shared__ int s_start[kMaxSeqPerLaunch + 1];  // first step per sequence; s_start[batch] = total steps
@@ -131,7 +139,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   const int H = p.num_heads;
   const int max_ctx = p.max_blocks * p.block_size;
 
-  // ---- block table into LDS and the step layout (a block-wide prefix sum over ceil(context / 64)). The lengths of
+  // ---- block table into LDS and the step layout (a block-wide prefix sum over ceil(context / 16)). The lengths of
   // the first kThreads sequences and every table entry a thread stages are loaded before any of them is waited for:
   // one round trip (a load-then-store loop waits for each load in turn, one round trip per kThreads entries).
   const int mb = p.max_blocks;
@@ -177,7 +185,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
     int row = row_first;
     const int raw = base == 0 ? ctx_first : (bb < p.batch ? seq_of(bb, row) : 0);
     const int ctx = bb < p.batch ? max(0, min(raw, max_ctx)) : 0;
-    const int n = (ctx + kStep - 1) / kStep;
+    const int n = (ctx + kTile - 1) / kTile;
     const int incl = wave_incl_scan(n, lane);
     int wmax = n;
 #pragma unroll
@@ -228,84 +236,90 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
 
   const int h = r16;
   const int hg = h < H ? h / p.group : -1;
-  uint16_t* vt = reinterpret_cast<uint16_t*>(lds_raw) + w * kTile * VROW;
+  uint16_t* vt = s_vt + w * kTile * VROW;
   // this lane's transposed-read address inside a d-tile: row jq*4 + r16/4, column 4*(r16%4)
   const uint16_t* vtr = vt + (jq * 4 + (r16 >> 2)) * VROW + 4 * (r16 & 3);
-  constexpr int kMOff = kWaves * kMaxHeads * kD;
-  constexpr int kLOff = kMOff + kWaves * kMaxHeads;
+  constexpr int kMOff = kMaxHeads * kD;  // inside a slot: O [16 heads][128], then m[16], l[16] (log2 domain)
+  constexpr int kLOff = kMOff + kMaxHeads;
+  // per-lane byte offsets of the tile loads: K row r16, dims jq*8 + [0, 8) (+ 32 per k-step); V piece 0 = row
+  // lane / PPR, dims (lane % PPR) * 8 + [0, 8)
+  const uint32_t koff = (uint32_t)(r16 * TT::ROW + jq * 8) * 2u;
+  const uint32_t voff = (uint32_t)((lane / TT::PPR) * TT::ROW + (lane % TT::PPR) * 8) * 2u;
+  const float c = p.scale_log2;
 
-  while (r < r1) {
-    const int ctx = uniform(s_ctx[b]);
-    const int64_t row = uniform(s_row[b]);
-    const int sb = uniform(s_start[b]);
-    const int nb = uniform(s_start[b + 1]) - sb;
-    if (nb == 0) {  // an empty row holds no step
-      ++b;
-      continue;
+  auto start_of = [&](int bs) { return uniform(s_start[bs]); };
+  auto next_nonempty = [&](int bs) {  // bs or the first sequence after it that holds a tile
+    while (start_of(bs + 1) == start_of(bs)) ++bs;
+    return bs;
+  };
+  // block id of range tile t of sequence bs
+  auto block_of = [&](int bs, int t) -> int64_t {
+    const int col = (t - start_of(bs)) * kTile / p.block_size;
+    if constexpr (BTL) return uniform(s_bt[bs * mb + col]);
+    else return p.block_tables[(int64_t)bs * p.bt_stride + col];
+  };
+  auto issue = [&](Tile<HK>& T, int64_t blk, int bs, int t) {  // loads of range tile t (sequence bs), block blk
+    T.ok = blk >= 0 && blk < p.num_blocks;
+    const int tok = (t - start_of(bs)) * kTile;
+    load_tile<HK>(T, p, (T.ok ? blk : 0) * p.block_size + (tok % p.block_size), koff, voff);
+  };
+  auto load_q = [&](u32x4 (&qv)[4], int bs) {  // query row of head r16: d = kq*32 + jq*8 + [0, 8)
+    const uint16_t* qb = p.q + (int64_t)uniform(s_row[bs]) * p.q_row_stride + (int64_t)(h < H ? h : 0) * kD + jq * 8;
+#pragma unroll
+    for (int kq = 0; kq < 4; ++kq) qv[kq] = ld_g16(qb + kq * 32);
+  };
+
+  int rr = r;   // round start (range position)
+  int bb = b;   // its sequence
+  while (rr < r1) {
+    // the round: up to kRoundSegs segments from rr
+    int re = rr, nseg = 0;
+    for (int bs = bb; nseg < kRoundSegs && re < r1; ++bs, ++nseg) {
+      bs = next_nonempty(bs);
+      re = min(r1, start_of(bs + 1));
     }
-    const int seg_end = min(r1, sb + nb);
-    const int tok0 = (r - sb) * kStep;
-    const int tok_end = min(ctx, (seg_end - sb) * kStep);
-    const bool whole = r == sb && seg_end == sb + nb;
-    const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
-    const int* bt_lds_row = s_bt + b * mb;
-    auto block_of = [&](int col) -> int64_t {
-      if constexpr (BTL) return uniform(bt_lds_row[col]);
-      else return bt_row[col];
-    };
+    const int R = re - rr;
+    auto share_lo = [&](int ww) { return rr + (int)(((int64_t)R * ww) / kWaves); };
+    const int t_lo = share_lo(w), t_hi = share_lo(w + 1);
 
-    // per-lane byte offsets of the tile loads: K row r16, dims jq*8 + [0, 8) (+ 32 per k-step); V piece 0 = row
-    // lane / PPR, dims (lane % PPR) * 8 + [0, 8)
-    const uint32_t koff = (uint32_t)(r16 * TT::ROW + jq * 8) * 2u;
-    const uint32_t voff = (uint32_t)((lane / TT::PPR) * TT::ROW + (lane % TT::PPR) * 8) * 2u;
-    // Issues the loads of the tile at token t0 of cache block blk.
-    auto issue = [&](Tile<HK>& T, int64_t blk, int t0) {
-      T.ok = blk >= 0 && blk < p.num_blocks;
-      load_tile<HK>(T, p, (T.ok ? blk : 0) * p.block_size + (t0 % p.block_size), koff, voff);
-    };
-
-    float m = -INFINITY;
-    float lsum = 0.f;
-    f32x4 acc[8];
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    // This wave's tiles: first, first + kStep, ... (a wave with none adds m = -inf, l = 0 to the merge). The query
-    // row and the first tile load together, the query first, so that building the score operands waits for it alone
-    // (all of this sits inside the branch: where a path without the tile loads joins, the compiler's wait counts
-    // would also cover the tile); the block id of the second tile is read meanwhile. Each later tile's loads go out
-    // as soon as the previous tile is computed, with the block id of the tile after it. Query row of head r16:
-    // d = kq*32 + jq*8 + [0, 8); the score B operand for k-step kc is piece kc % 4 when kc's kv head (kc / 4) is
-    // the lane's group, else zero: block-diagonal over (kv head, d).
-    const int first = tok0 + w * kTile;
-    if (first < tok_end) {
-      u32x4 qv[4];
-      {
-        const uint16_t* qb = p.q + row * p.q_row_stride + (int64_t)(h < H ? h : 0) * kD + jq * 8;
-#pragma unroll
-        for (int kq = 0; kq < 4; ++kq) qv[kq] = ld_g16(qb + kq * 32);
+    if (t_lo < t_hi) {
+      // this wave's first tile: sequence bc (round segment kc)
+      int bc = next_nonempty(bb), kc = 0;
+      while (start_of(bc + 1) <= t_lo) {
+        bc = next_nonempty(bc + 1);
+        ++kc;
       }
       Tile<HK> T;
-      issue(T, block_of(first / p.block_size), first);
-      int64_t blk_next = block_of(min(first + kStep, tok_end - 1) / p.block_size);
-      u32x4 qop[TT::KC];
-#pragma unroll
-      for (int kc = 0; kc < TT::KC; ++kc) qop[kc] = hg == kc / 4 ? qv[kc % 4] : zero4();
-      const float c = p.scale_log2;
+      u32x4 qv[4];
+      load_q(qv, bc);
+      issue(T, block_of(bc, t_lo), bc, t_lo);
+      // the tile to issue next (t_lo + 1: sequence bi) and its block id, read one tile ahead
+      int bi = bc;
+      if (t_lo + 1 < t_hi && t_lo + 1 >= start_of(bc + 1)) bi = next_nonempty(bc + 1);
+      int64_t blk_pf = t_lo + 1 < t_hi ? block_of(bi, t_lo + 1) : 0;
 
-      // Scores, online softmax and P V of one loaded tile. The scale goes into the exp2 argument (one FMA); the running
-      // max moves (rescaling acc and lsum) only when the tile max exceeds it by more than 8 in log2 units (p <= 256,
-      // exact after the final 1 / l); the masks and zero selects run only on a tile that is not fully valid.
-      auto compute = [&](const Tile<HK>& T, int t0) {
+      float m = -INFINITY;
+      float lsum = 0.f;
+      f32x4 acc[8];
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      u32x4 qop[TT::KC];
+      bool fresh = true;  // the score operands of sequence bc are still to be built from qv
+
+      // Scores, online softmax and P V of one loaded tile whose first token is t0 of a sequence of ctx tokens. The
+      // scale goes into the exp2 argument (one FMA); the running max moves (rescaling acc and lsum) only when the
+      // tile max exceeds it by more than 8 in log2 units (p <= 256, exact after the final 1 / l); the masks and zero
+      // selects run only on a tile that is not fully valid.
+      auto compute = [&](const Tile<HK>& T, int t0, int tok_end) {
         f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kc = 0; kc < TT::KC; ++kc) s = mfma_16x16x32(T.k[kc], qop[kc], s);
+        for (int kk = 0; kk < TT::KC; ++kk) s = mfma_16x16x32(T.k[kk], qop[kk], s);
         const bool full = T.ok && t0 + kTile <= tok_end;  // wave-uniform
         // lane (head r16) holds tokens t0 + jq*4 + [0, 4)
         float x[4];
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          x[rr] = full || (T.ok && (t0 + jq * 4 + rr) < tok_end) ? s[rr] : -INFINITY;
+        for (int q4 = 0; q4 < 4; ++q4)
+          x[q4] = full || (T.ok && (t0 + jq * 4 + q4) < tok_end) ? s[q4] : -INFINITY;
         const float tm = col_max4(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]))) * c;
         const bool up = tm > m + 8.f;
         if (__builtin_amdgcn_ballot_w64(up) != 0) {  // wave-uniform
@@ -318,9 +332,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
         const float mu = m == -INFINITY ? 0.f : m;
         float ps = 0.f;
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          x[rr] = fast_exp2(fmaf(x[rr], c, -mu));
-          ps += x[rr];
+        for (int q4 = 0; q4 < 4; ++q4) {
+          x[q4] = fast_exp2(fmaf(x[q4], c, -mu));
+          ps += x[q4];
         }
         lsum += ps;
 
@@ -362,68 +376,117 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
         wave_lds_sync();
       };
 
-      for (int t0 = first; t0 < tok_end; t0 += kStep) {
-        compute(T, t0);
-        if (t0 + kStep < tok_end) {
-          issue(T, blk_next, t0 + kStep);
-          blk_next = block_of(min(t0 + 2 * kStep, tok_end - 1) / p.block_size);
+      for (int t = t_lo; t < t_hi; ++t) {
+        if (fresh) {  // a new sequence: block-diagonal query operands (kk's kv head kk / 4)
+#pragma unroll
+          for (int kk = 0; kk < TT::KC; ++kk) qop[kk] = hg == kk / 4 ? qv[kk % 4] : zero4();
+          fresh = false;
+        }
+        const int sbc = start_of(bc);
+        compute(T, (t - sbc) * kTile, uniform(s_ctx[bc]));
+        // the next tile's loads go out now, with the query first when it starts a new sequence; then the block id
+        // of the tile after it
+        if (t + 1 < t_hi) {
+          if (bi != bc) load_q(qv, bi);
+          issue(T, blk_pf, bi, t + 1);
+          int bn = bi;
+          if (t + 2 < t_hi && t + 2 >= start_of(bi + 1)) bn = next_nonempty(bi + 1);
+          blk_pf = t + 2 < t_hi ? block_of(bn, t + 2) : 0;
+          const bool seq_done = bi != bc;
+          if (seq_done) {  // sequence bc's share of this wave is done: its partial goes to slot w + kc
+            lsum = col_sum4(lsum);
+            float* sl = s_slot + (w + kc) * kPartialFloats;
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(&sl[r16 * kD + dt * 16 + jq * 4]) = acc[dt];
+            if (jq == 0) {
+              sl[kMOff + r16] = m;
+              sl[kLOff + r16] = lsum;
+            }
+            m = -INFINITY;
+            lsum = 0.f;
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            fresh = true;
+            bc = bi;
+            ++kc;
+          }
+          bi = bn;
+        }
+      }
+      lsum = col_sum4(lsum);  // the last sequence of the share
+      float* sl = s_slot + (w + kc) * kPartialFloats;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(&sl[r16 * kD + dt * 16 + jq * 4]) = acc[dt];
+      if (jq == 0) {
+        sl[kMOff + r16] = m;
+        sl[kLOff + r16] = lsum;
+      }
+    }
+    __syncthreads();  // every wave's partials of the round are in LDS
+
+    // ---- merge the round's segments (fp32); thread (head hh, dims d0 .. d0 + kDpt) ----
+    constexpr int kDpt = kMaxHeads * kD / kThreads;  // output dims per thread
+    constexpr int kTpr = kD / kDpt;                    // threads per head
+    const int hh = tid / kTpr;
+    const int d0 = (tid % kTpr) * kDpt;
+    int bs = bb;
+    for (int k = 0; k < nseg; ++k, ++bs) {
+      bs = next_nonempty(bs);
+      const int sb = start_of(bs), eb = start_of(bs + 1);
+      const int a = max(rr, sb), e = min(re, eb);
+      // the waves whose shares hold tiles of this segment, read in one pass (all loads before any use)
+      float mw[kWaves], lw[kWaves];
+      f32x4 ow[kWaves][kDpt / 4];
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ++ww) {
+        const bool touched = share_lo(ww) < e && share_lo(ww + 1) > a && share_lo(ww) < share_lo(ww + 1);
+        // (a slot no wave wrote in this launch holds whatever LDS held: its values are selected away, never scaled)
+        const float* sl = s_slot + (touched ? ww + k : k) * kPartialFloats;
+        mw[ww] = touched ? sl[kMOff + hh] : -INFINITY;
+        lw[ww] = touched ? sl[kLOff + hh] : 0.f;
+#pragma unroll
+        for (int i = 0; i < kDpt / 4; ++i) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(&sl[hh * kD + d0 + 4 * i]);
+          ow[ww][i] = touched ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+      float M = -INFINITY;
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, mw[ww]);
+      const float Mu = M == -INFINITY ? 0.f : M;
+      float L = 0.f;
+      f32x4 o[kDpt / 4];
+#pragma unroll
+      for (int i = 0; i < kDpt / 4; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ++ww) {
+        const float ew = fast_exp2(mw[ww] - Mu);  // 0 (and lw, ow 0) for the waves that did not touch the segment
+        L += ew * lw[ww];
+#pragma unroll
+        for (int i = 0; i < kDpt / 4; ++i) o[i] += ew * ow[ww][i];
+      }
+      if (a == sb && e == eb) {  // the whole sequence is in this workgroup's range: the output itself
+        if (hh < H) {
+          const float inv = L > 0.f ? 1.f / L : 0.f;
+          const int64_t row = uniform(s_row[bs]);
+#pragma unroll
+          for (int i = 0; i < kDpt / 4; ++i)
+            *reinterpret_cast<u32x2*>(p.out + row * p.out_row_stride + (int64_t)hh * kD + d0 + 4 * i) =
+                u32x2{pack_bf16x2(o[i][0] * inv, o[i][1] * inv), pack_bf16x2(o[i][2] * inv, o[i][3] * inv)};
+        }
+      } else {  // cut by a range boundary: partial for decode_merge_kernel, slot b + g
+        float* part = p.partials + (int64_t)(bs + g) * kPartialFloats;
+#pragma unroll
+        for (int i = 0; i < kDpt / 4; ++i) *reinterpret_cast<f32x4*>(&part[hh * kD + d0 + 4 * i]) = o[i];
+        if (tid % kTpr == 0) {
+          part[kMOff + hh] = M;
+          part[kLOff + hh] = L;
         }
       }
     }
-
-    // ---- merge the waves (fp32, in LDS); thread (head hh, dims d0 .. d0 + kDpt) ----
-    constexpr int kDpt = kMaxHeads * kD / kThreads;  // output dims per thread
-    constexpr int kTpr = kD / kDpt;                    // threads per head
-    lsum = col_sum4(lsum);
-    float* red = reinterpret_cast<float*>(lds_raw);
-    const int hh = tid / kTpr;
-    const int d0 = (tid % kTpr) * kDpt;
-    __syncthreads();
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-      *reinterpret_cast<f32x4*>(&red[(w * kMaxHeads + r16) * kD + dt * 16 + jq * 4]) = acc[dt];
-    if (jq == 0) {
-      red[kMOff + w * kMaxHeads + r16] = m;
-      red[kLOff + w * kMaxHeads + r16] = lsum;
-    }
-    __syncthreads();
-    float M = -INFINITY;
-#pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, red[kMOff + ww * kMaxHeads + hh]);
-    const float Mu = M == -INFINITY ? 0.f : M;
-    float L = 0.f;
-    f32x4 o[kDpt / 4];
-#pragma unroll
-    for (int i = 0; i < kDpt / 4; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) {
-      const float e = fast_exp2(red[kMOff + ww * kMaxHeads + hh] - Mu);
-      L += e * red[kLOff + ww * kMaxHeads + hh];
-#pragma unroll
-      for (int i = 0; i < kDpt / 4; ++i)
-        o[i] += e * *reinterpret_cast<const f32x4*>(&red[(ww * kMaxHeads + hh) * kD + d0 + 4 * i]);
-    }
-    if (whole) {
-      if (hh < H) {
-        const float inv = L > 0.f ? 1.f / L : 0.f;
-#pragma unroll
-        for (int i = 0; i < kDpt / 4; ++i)
-          *reinterpret_cast<u32x2*>(p.out + row * p.out_row_stride + (int64_t)hh * kD + d0 + 4 * i) =
-              u32x2{pack_bf16x2(o[i][0] * inv, o[i][1] * inv), pack_bf16x2(o[i][2] * inv, o[i][3] * inv)};
-      }
-    } else {  // cut by a range boundary: partial for decode_merge_kernel, slot b + g
-      float* part = p.partials + (int64_t)(b + g) * kPartialFloats;
-#pragma unroll
-      for (int i = 0; i < kDpt / 4; ++i) *reinterpret_cast<f32x4*>(&part[hh * kD + d0 + 4 * i]) = o[i];
-      if (tid % kTpr == 0) {
-        part[kMaxHeads * kD + hh] = M;
-        part[kMaxHeads * kD + kMaxHeads + hh] = L;
-      }
-    }
-    __syncthreads();  // LDS is free for the next sequence
-
-    r = seg_end;
-    ++b;
+    __syncthreads();  // the slots and V tiles are free for the next round
+    rr = re;
+    bb = bs;
   }
 }
 
