@@ -4,7 +4,6 @@
 // returns a status (VOX_OK, VOX_EINVAL, VOX_EHIP) instead of throwing; vox_last_error() gives the calling thread's
 // message for the last failure. Nothing here allocates, frees or synchronizes, so every call can be captured into
 // a HIP graph.
-#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -34,47 +33,6 @@ int hip_status(hipError_t e, const char* what) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// A second stream per device on which a mixed step's prefill rows run beside its decode rows: forked from the
-// caller's stream by an event and joined back by another, so the call stays ordered on the caller's stream and can
-// be captured into a HIP graph (the fork and join become graph edges). Default priority, non-blocking.
-struct AuxStream {
-  std::atomic<bool> ready{false};
-  std::mutex mu;  // one fork / join sequence at a time (the events are shared)
-  hipStream_t stream = nullptr;
-  hipEvent_t fork = nullptr;
-  hipEvent_t join = nullptr;
-};
-constexpr int kMaxDevices = 64;
-AuxStream g_aux[kMaxDevices];
-std::mutex g_aux_create;
-
-// The current device's aux stream, created on its first use outside a capture (creating a stream or event is not an
-// operation a capture can hold); nullptr when there is none, and the caller then runs everything on its own stream.
-AuxStream* aux_stream(hipStream_t caller) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  AuxStream& a = g_aux[dev];
-  if (a.ready.load(std::memory_order_acquire)) return &a;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(caller, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  std::lock_guard<std::mutex> lk(g_aux_create);
-  if (!a.ready.load(std::memory_order_relaxed)) {
-    if (hipStreamCreateWithFlags(&a.stream, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&a.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&a.join, hipEventDisableTiming) != hipSuccess) {
-      (void)hipGetLastError();
-      return nullptr;
-    }
-    a.ready.store(true, std::memory_order_release);
-  }
-  return &a;
-}
 
 constexpr int kHeadDim = 128;
 constexpr int kMaxHeads = 16;
@@ -228,6 +186,7 @@ size_t vox_prefill_workspace_bytes(int batch) { return vox_decode_workspace_byte
 // names a host-side stand-in, not the device array: its device address on each GPU comes from hipGetSymbolAddress,
 // looked up once per device with that device current, and only that address is handed to kernels.
 namespace {
+constexpr int kMaxDevices = 64;
 constexpr size_t kScratchBytes = size_t(16) << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 void* g_scratch_ptr[kMaxDevices] = {};
@@ -396,27 +355,11 @@ int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const
     d.out_row_stride = out_row_stride;
     d.cu_q = cu_seqlens_q;
     d.cu_k = cu_seqlens_k;
-    if (max_seqlen_q <= 1) return launch_decode_slices(d, batch, num_kv_heads, workspace, s);
-    // Both kinds of rows: the decode kernels (memory-bound, one workgroup per CU) go out first on the caller's
-    // stream, the prefill rows (MFMA- and LDS-bound) beside them on the aux stream, so the two share the CUs.
-    AuxStream* aux = aux_stream(s);
-    if (!aux) {
+    if (max_seqlen_q > 1) {
       const int sp = hip_status(vox::launch_prefill(a, max_seqlen_q, s), "prefill_attn launch");
       if (sp != VOX_OK) return sp;
-      return launch_decode_slices(d, batch, num_kv_heads, workspace, s);
     }
-    std::lock_guard<std::mutex> lk(aux->mu);
-    int st = hip_status(hipEventRecord(aux->fork, s), "prefill_attn fork");
-    if (st == VOX_OK) st = hip_status(hipStreamWaitEvent(aux->stream, aux->fork, 0), "prefill_attn fork");
-    if (st != VOX_OK) return st;
-    const int sd = launch_decode_slices(d, batch, num_kv_heads, workspace, s);
-    const int sp = hip_status(vox::launch_prefill(a, max_seqlen_q, aux->stream), "prefill_attn launch");
-    // the join is recorded whatever happened above, so the caller's stream never runs ahead of the aux stream's work
-    st = hip_status(hipEventRecord(aux->join, aux->stream), "prefill_attn join");
-    if (st == VOX_OK) st = hip_status(hipStreamWaitEvent(s, aux->join, 0), "prefill_attn join");
-    if (sd != VOX_OK) return sd;
-    if (sp != VOX_OK) return sp;
-    return st;
+    return launch_decode_slices(d, batch, num_kv_heads, workspace, s);
   }
   return hip_status(vox::launch_prefill(a, max_seqlen_q, s), "prefill_attn launch");
 }

@@ -628,36 +628,117 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
 // uneven numbers of empty tiles). A causal run starts at each sequence's last query tile, the one with the most key
 // tiles, so the light tiles fill the end of the run instead of the heavy ones (16 x 2048 tokens -3 %, 2 x 8192 -5 %).
 // Persistent (PER): a fixed grid, for calls whose (q tile, sequence) grid would be mostly empty (a mixed step's
-// decode rows, left to the decode kernel): each workgroup scans cu_q once, numbers the items of the sequences that
-// have work (heaviest causal q tile first within a sequence, both kv heads of a tile together), and takes every
-// gridDim.x-th item from its own index on. An empty workgroup of the plain grid costs a memory round trip to find
-// it has nothing to do; a grid of a few thousand of them took longer than the work itself.
+// decode rows, left to the decode kernel): each workgroup reads cu_q once, numbers the items of the sequences that
+// have work and walks its share of them (order below). An empty workgroup of the plain grid costs a memory round
+// trip to find it has nothing to do; a grid of a few thousand of them took longer than the work itself.
 template <bool QUANT, int KV, int NW, int RT, bool PER>
 __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 : 2) void prefill_kernel(PrefillArgs p) {
   if constexpr (PER) {
     constexpr int NTH = 64 * NW * (QUANT ? 2 : 1);
     constexpr int ROWS = 16 * RT * NW;
-    __shared__ int s_first[kMaxSeqPerLaunch + 1];  // first item of each sequence; s_first[batch] = the total
-    __shared__ int s_wtot[NTH / 64];
+    constexpr int kRankCap = 1024;  // longest sequence, in q tiles, that the rank order covers
+    __shared__ int s_nt[kMaxSeqPerLaunch];       // q tiles of each sequence (0: nothing for this kernel)
+    __shared__ int s_act[kMaxSeqPerLaunch];      // the sequences with q tiles, in order
+    __shared__ int s_sorted[kMaxSeqPerLaunch];   // ... most tiles first (stable)
+    __shared__ int s_snt[kMaxSeqPerLaunch];      // their tile counts
+    __shared__ int s_P[kRankCap + 1];            // items of the ranks before r
+    __shared__ int s_red[2 * (NTH / 64)];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int BQ = ROWS / p.group;
     const int HKz = QUANT ? 1 : p.num_kv_heads;
-    int run = 0;
+    // q tiles per sequence; the sequences that have any, compacted in order (a block-wide scan); the most tiles
+    int maxnt = 0, nact = 0, run = 0;
     for (int base = 0; base < p.batch; base += NTH) {
       const int bb = base + tid;
-      int n = 0;
+      int nt = 0;
       if (bb < p.batch) {
         const int nq = max(p.cu_q[bb + 1] - p.cu_q[bb], 0);
-        n = (p.skip_single && nq == 1) ? 0 : (nq + BQ - 1) / BQ * HKz;
+        nt = (p.skip_single && nq == 1) ? 0 : (nq + BQ - 1) / BQ;
+        s_nt[bb] = nt;
       }
-      const int incl = wave_incl_scan(n, lane);
-      if (lane == kWave - 1) s_wtot[w] = incl;
+      const int incl = wave_incl_scan(nt > 0 ? 1 : 0, lane);
+      int wmax = nt;
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) wmax = max(wmax, __shfl_xor(wmax, o, kWave));
+      if (lane == kWave - 1) {
+        s_red[w] = incl;
+        s_red[NTH / 64 + w] = wmax;
+      }
       __syncthreads();
       int before = 0, total = 0;
 #pragma unroll
       for (int ww = 0; ww < NTH / 64; ++ww) {
-        before += ww < w ? s_wtot[ww] : 0;
-        total += s_wtot[ww];
+        before += ww < w ? s_red[ww] : 0;
+        total += s_red[ww];
+        maxnt = max(maxnt, s_red[NTH / 64 + ww]);
+      }
+      if (nt > 0) s_act[run + before + incl - 1] = bb;
+      run += total;
+      __syncthreads();
+    }
+    nact = __builtin_amdgcn_readfirstlane(run);
+    maxnt = __builtin_amdgcn_readfirstlane(maxnt);
+    // Items in rank order: rank r holds the r-th heaviest q tile (causal: the r-th from the end) of every sequence
+    // that has more than r tiles, sequences with the most tiles first, both kv heads of a tile together. With the
+    // sequences sorted by tile count, rank r is the first c(r) = #{nt > r} of them, and P(r) = HKz sum min(nt, r)
+    // items come before it. Walking this order in a snake over the workgroups (g, 2G - 1 - g, 2G + g, ...) hands the
+    // heaviest tiles out first and pairs heavy with light ones: for a mixed step's 6 prefills of 300-600 tokens the
+    // most a workgroup walks drops from 14 key tiles (sequence by sequence) to 9, the heaviest single item.
+    // Longer sequences than kRankCap tiles keep the sequence-by-sequence order.
+    const bool ranked = maxnt <= kRankCap;
+    if (ranked) {
+      for (int a = tid; a < nact; a += NTH) {  // stable rank of each active sequence by tile count
+        const int bb = s_act[a];
+        const int nt = s_nt[bb];
+        int pos = 0;
+#pragma unroll 8
+        for (int a2 = 0; a2 < nact; ++a2) {
+          const int n2 = s_nt[s_act[a2]];
+          pos += n2 > nt || (n2 == nt && a2 < a);
+        }
+        s_sorted[pos] = bb;
+        s_snt[pos] = nt;
+      }
+      __syncthreads();
+      for (int r = tid; r <= maxnt; r += NTH) {
+        int sum = 0;
+#pragma unroll 8
+        for (int j = 0; j < nact; ++j) sum += min(s_snt[j], r);
+        s_P[r] = sum * HKz;
+      }
+      __syncthreads();
+      const int W = __builtin_amdgcn_readfirstlane(s_P[maxnt]);
+      const int G = gridDim.x, g = blockIdx.x;
+      for (int t = 0; t * G < W; ++t) {
+        const int k = t * G + ((t & 1) ? G - 1 - g : g);
+        if (k >= W) continue;
+        int lo = 0, hi = maxnt;  // the rank r with s_P[r] <= k < s_P[r + 1]
+        while (hi - lo > 1) {
+          const int mid = (lo + hi) >> 1;
+          if (__builtin_amdgcn_readfirstlane(s_P[mid]) <= k) lo = mid; else hi = mid;
+        }
+        const int local = k - __builtin_amdgcn_readfirstlane(s_P[lo]);
+        const int bq = __builtin_amdgcn_readfirstlane(s_sorted[local / HKz]);
+        const int nt = __builtin_amdgcn_readfirstlane(s_nt[bq]);
+        prefill_tile<QUANT, KV, NW, RT>(p, p.causal ? nt - 1 - lo : lo, bq, local % HKz);
+        __syncthreads();  // the item's LDS is free for the next one
+      }
+      return;
+    }
+    // sequence-by-sequence order (heaviest causal q tile first within a sequence), every gridDim.x-th item
+    __shared__ int s_first[kMaxSeqPerLaunch + 1];  // first item of each sequence; s_first[batch] = the total
+    run = 0;
+    for (int base = 0; base < p.batch; base += NTH) {
+      const int bb = base + tid;
+      const int n = bb < p.batch ? s_nt[bb] * HKz : 0;
+      const int incl = wave_incl_scan(n, lane);
+      if (lane == kWave - 1) s_red[w] = incl;
+      __syncthreads();
+      int before = 0, total = 0;
+#pragma unroll
+      for (int ww = 0; ww < NTH / 64; ++ww) {
+        before += ww < w ? s_red[ww] : 0;
+        total += s_red[ww];
       }
       if (bb < p.batch) s_first[bb] = run + before + incl - n;
       run += total;
