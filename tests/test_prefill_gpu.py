@@ -419,18 +419,22 @@ def test_mixed_step_captured_in_a_hip_graph_replays_like_eager():
 def test_mixed_step_with_a_prefill_longer_than_the_rank_order_covers():
     """A mixed step (one-query rows on the decode kernels) whose prefill spans more than 1024 query tiles takes the
     persistent prefill's sequence-by-sequence order: 16 query heads over 1 kv head (4 tokens per tile), a 4200-token
-    prefill beside two decode rows; its first and last 100 query rows are checked against the oracle."""
+    prefill beside ten decode rows; its first and last 100 query rows are checked against the oracle."""
     gen = torch.Generator().manual_seed(92)
     H1, HK1 = 16, 1
     n = 4200
-    nq, nk = [n, 1, 1], [n, 300, 77]
-    kc = randn(gen, 24, BLOCK, HK1, D)
-    vc = randn(gen, 24, BLOCK, HK1, D)
-    perm = torch.randperm(24, generator=gen).tolist()
-    tables = torch.full((3, 17), -1, dtype=torch.int32)
-    tables[0, :17] = torch.tensor(perm[:17])
-    tables[1, :2] = torch.tensor(perm[17:19])
-    tables[2, :1] = torch.tensor(perm[19:20])
+    dec = [300, 77, 1, 256, 257, 900, 5, 600, 1000, 2]
+    nq, nk = [n] + [1] * len(dec), [n] + dec
+    pool = 17 + sum((x + BLOCK - 1) // BLOCK for x in dec) + 2
+    kc = randn(gen, pool, BLOCK, HK1, D)
+    vc = randn(gen, pool, BLOCK, HK1, D)
+    perm = torch.randperm(pool, generator=gen).tolist()
+    tables = torch.full((len(nk), 17), -1, dtype=torch.int32)
+    at = 0
+    for b, x in enumerate(nk):
+        nb = (x + BLOCK - 1) // BLOCK
+        tables[b, :nb] = torch.tensor(perm[at:at + nb])
+        at += nb
     q = randn(gen, sum(nq), H1, D)
     out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), _cu(nq).to(DEV), _cu(nk).to(DEV), max(nq),
                                  max(nk), softmax_scale=SCALE, causal=True, block_table=tables.to(DEV)).cpu()
@@ -439,5 +443,5 @@ def test_mixed_step_with_a_prefill_longer_than_the_rank_order_covers():
     for i0, i1 in ((0, 100), (n - 100, n)):
         want = ref.attend(q[i0:i1].float(), k0[:i1], v0[:i1], causal=True, scale=SCALE).view(i1 - i0, H1, D)
         attn_close(out[i0:i1], want, f"long prefill rows {i0}:{i1}")
-    want = ref.varlen(q[n:].float(), [0, 1, 2], _cu(nk[1:]), k_cache=kc, v_cache=vc, block_tables=tables[1:])
+    want = ref.varlen(q[n:].float(), _cu(nq[1:]), _cu(nk[1:]), k_cache=kc, v_cache=vc, block_tables=tables[1:])
     attn_close(out[n:], want, "decode rows beside the long prefill")
