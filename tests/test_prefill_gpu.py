@@ -179,6 +179,31 @@ def test_group_sizes(h, hk):
     attn_close(out, ref.varlen(q.float(), _cu(lens), _cu(lens), k=k, v=v), f"H={h} HK={hk}")
 
 
+@pytest.mark.parametrize("h,hk,paged", [(16, 2, False), (16, 2, True), (16, 1, False), (16, 4, True)])
+def test_rank_major_grid_of_causal_items_beyond_two_per_cu(h, hk, paged):
+    """Causal grids of 64-row work items that exceed two per CU (512 on an MI355X) but not four run rank-major, the
+    heaviest q tile of every (sequence, kv head) first: group sizes 16, 8 and 4, packed and paged with cached
+    prefixes (bottom-right aligned), sequences of very different lengths (the short ones' high ranks are empty)."""
+    gen = torch.Generator().manual_seed(61 + h + hk + paged)
+    nq = [200, 3, 500, 77, 300, 129] if hk < 4 else [600, 1, 310, 64]
+    pre = [50, 0, 300, 10, 0, 1] if paged else [0] * len(nq)
+    nk = [a + b for a, b in zip(nq, pre)]
+    g = h // hk
+    assert 512 < -(-max(nq) // (64 // g)) * len(nq) * hk <= 1024  # the rank-major form on a 256-CU part
+    q = randn(gen, sum(nq), h, D)
+    if paged:
+        kc, vc, tables = paged_pool(gen, nk, sum(-(-n // BLOCK) for n in nk) + 2, hk=hk)
+        out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), _cu(nq).to(DEV), _cu(nk).to(DEV), max(nq),
+                                     max(nk), softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
+        want = ref.varlen(q.float(), _cu(nq), _cu(nk), k_cache=kc, v_cache=vc, block_tables=tables)
+    else:
+        k, v = randn(gen, sum(nk), hk, D), randn(gen, sum(nk), hk, D)
+        out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), _cu(nq).to(DEV), _cu(nk).to(DEV), max(nq),
+                                     max(nk), softmax_scale=SCALE, causal=True)
+        want = ref.varlen(q.float(), _cu(nq), _cu(nk), k=k, v=v)
+    attn_close(out, want, f"rank-major H={h} HK={hk} paged={paged}")
+
+
 def test_long_sequences_compute_bound_shape():
     """Longer sequences (the compute-bound prefill shape the bench also reports): 4 x U[1024, 2048] tokens."""
     gen = torch.Generator().manual_seed(55)

@@ -51,6 +51,10 @@ constexpr unsigned kXcdOrderMinWorkgroups = 1024;
 // 12.2 us, 44 x 46 paged over a 50-token prefix -4 %, 16 x 512 -3 %, 4 x 2048 -4 %, 2 x 8192 -3 %; at 4096
 // workgroups (16 x 2048, 64 x 512) the 4-wave form is 2-3 % faster).
 constexpr int64_t kSmallGridWorkgroups = 2048;
+// Grid forms of prefill_kernel (below)
+constexpr int kFormGrid = 0;
+constexpr int kFormPersistent = 1;
+constexpr int kFormRanked = 2;
 
 // Where a workgroup's keys come from (one kernel instance each, so no path's loop-carried state constrains another's
 // load waits): packed [Tk, HK, D] rows; the paged cache with block_size a multiple of 64 (a 64-key tile lies in one
@@ -622,18 +626,28 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
   }
 }
 
-// Grid forms. Non-persistent: one workgroup per (q tile, sequence, kv head) of the grid. Workgroup i runs on XCD
+// Grid forms. Plain grid (kFormGrid): one workgroup per (q tile, sequence, kv head) of the grid. Workgroup i runs on XCD
 // i % 8; with xcd_order each XCD gets a contiguous run of work items, so the query tiles that re-read a sequence's
 // K/V tiles find them in that XCD's L2 (the launcher sets it for large grids; on small ones the runs would hold
 // uneven numbers of empty tiles). A causal run starts at each sequence's last query tile, the one with the most key
 // tiles, so the light tiles fill the end of the run instead of the heavy ones (16 x 2048 tokens -3 %, 2 x 8192 -5 %).
-// Persistent (PER): a fixed grid, for calls whose (q tile, sequence) grid would be mostly empty (a mixed step's
-// decode rows, left to the decode kernel): each workgroup reads cu_q once, numbers the items of the sequences that
-// have work and walks its share of them (order below). An empty workgroup of the plain grid costs a memory round
+// Persistent (kFormPersistent): a fixed grid, for calls whose (q tile, sequence) grid would be mostly empty (a mixed
+// step's decode rows, left to the decode kernel): each workgroup reads cu_q once, numbers the items of the sequences
+// that have work and walks its share of them (order below). An empty workgroup of the plain grid costs a memory round
 // trip to find it has nothing to do; a grid of a few thousand of them took longer than the work itself.
-template <bool QUANT, int KV, int NW, int RT, bool PER>
+// Rank-major (kFormRanked): a causal grid of more work items than fit on the CUs at once, one 1-D grid in rank order:
+// rank r = the r-th heaviest q tile of every (sequence, kv head), so the longest chains of key tiles start first
+// and the light tiles fill in behind them (with the plain grid, the second kv head's heavy tiles waited for a free
+// slot: config 2, 832 items on 512 slots, 16.5 -> 13.4 us). Within a rank the (sequence, kv head) pairs rotate by
+// r, so a pair's tiles are dealt over all eight XCDs rather than all landing on one. A form of its own: the extra
+// index arithmetic in the plain grid's kernel cost the short non-causal steps 4-7 %.
+template <bool QUANT, int KV, int NW, int RT, int FORM>
 __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 : 2) void prefill_kernel(PrefillArgs p) {
-  if constexpr (PER) {
+  if constexpr (FORM == kFormRanked) {
+    const int n = p.batch * p.num_kv_heads, id = blockIdx.x, r = id / n, c = (id + r) % n;
+    const int qt = p.causal ? (int)gridDim.x / n - 1 - r : r;
+    prefill_tile<QUANT, KV, NW, RT>(p, qt, c / p.num_kv_heads, c % p.num_kv_heads);
+  } else if constexpr (FORM == kFormPersistent) {
     constexpr int NTH = 64 * NW * (QUANT ? 2 : 1);
     constexpr int ROWS = 16 * RT * NW;
     constexpr int kRankCap = 1024;  // longest sequence, in q tiles, that the rank order covers
@@ -787,15 +801,15 @@ static int device_cus() {
   return cus;
 }
 
-template <bool QUANT, int NW, int RT, bool PER = false>
+template <bool QUANT, int NW, int RT, int FORM = kFormGrid>
 hipError_t launch_prefill_kind(const PrefillArgs& a, dim3 grid, hipStream_t stream) {
   const dim3 block(64 * NW * (QUANT ? a.num_kv_heads : 1));
   if (!a.block_tables)
-    prefill_kernel<QUANT, kPacked, NW, RT, PER><<<grid, block, 0, stream>>>(a);
+    prefill_kernel<QUANT, kPacked, NW, RT, FORM><<<grid, block, 0, stream>>>(a);
   else if (a.block_size % kBK == 0)
-    prefill_kernel<QUANT, kPagedTiles, NW, RT, PER><<<grid, block, 0, stream>>>(a);
+    prefill_kernel<QUANT, kPagedTiles, NW, RT, FORM><<<grid, block, 0, stream>>>(a);
   else
-    prefill_kernel<QUANT, kPagedPieces, NW, RT, PER><<<grid, block, 0, stream>>>(a);
+    prefill_kernel<QUANT, kPagedPieces, NW, RT, FORM><<<grid, block, 0, stream>>>(a);
   return hipGetLastError();
 }
 
@@ -815,7 +829,7 @@ hipError_t launch_prefill(const PrefillArgs& a0, int max_seqlen_q, hipStream_t s
       if (s.block_tables) s.block_tables = a.block_tables + (int64_t)b0 * a.bt_stride;
       const int64_t items = ((int64_t)max_seqlen_q + bq - 1) / bq * s.batch * s.num_kv_heads;
       const int64_t grid = items < 2 * device_cus() ? items : 2 * device_cus();
-      const hipError_t e = launch_prefill_kind<false, 4, 1, true>(s, dim3((unsigned)grid), stream);
+      const hipError_t e = launch_prefill_kind<false, 4, 1, kFormPersistent>(s, dim3((unsigned)grid), stream);
       if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -825,12 +839,15 @@ hipError_t launch_prefill(const PrefillArgs& a0, int max_seqlen_q, hipStream_t s
   // (measured: head-start step 200 x 7 tokens 7.4 -> 6.8 us, LocEnc 150 x 5 6.1 -> 5.5 us). Up to four per CU when
   // the longest sequence spans 16+ such tiles: halving a workgroup's rows halves the work of its chain of key tiles
   // (config 2: 16.9 -> 16.2 us), while on short sequences the doubled tile loads cost more than that saves (44 x 46
-  // tokens paged 12.8 -> 14.0 us, LocDiT 150 x 11 8.4 -> 10.0 us with the wider rule).
+  // tokens paged 12.8 -> 14.0 us, LocDiT 150 x 11 8.4 -> 10.0 us with the wider rule). A causal grid beyond two per
+  // CU runs rank-major (heaviest q tiles first).
   const bool fits64 = 64 % a.group == 0;  // group sizes above 64 take the 128-row form only
   const int64_t tiles64 = fits64 ? (max_seqlen_q + 64 / a.group - 1) / (64 / a.group) : 0;
   const int64_t grid64 = tiles64 * a.batch * a.num_kv_heads, cus = device_cus();
   if (fits64 && (grid64 <= 2 * cus || (grid64 <= 4 * cus && tiles64 >= 16))) {
     a.xcd_order = 0;
+    if (a.causal && grid64 > 2 * cus && grid64 <= INT32_MAX)
+      return launch_prefill_kind<false, 4, 1, kFormRanked>(a, dim3((unsigned)grid64), stream);
     return launch_prefill_kind<false, 4, 1>(a, dim3((unsigned)tiles64, (unsigned)a.batch, (unsigned)a.num_kv_heads),
                                             stream);
   }
