@@ -165,3 +165,29 @@ def test_int8_sixteen_row_halves_over_several_key_tiles(bs):
                                       max(lens), SCALE, quant=True, inv_smooth=inv.to(DEV))
         want = ref.varlen(q.float(), cu, cu, k_cache=kc, v_cache=vc, block_tables=tables)
     _check(out, want, f"16-row int8, block_size {bs}", inv)
+
+
+@pytest.mark.parametrize("bs,h,hk", [(None, 16, 2), (256, 16, 2), (96, 16, 2), (None, 8, 1)])
+def test_int8_rank_major_grid_beyond_one_item_per_cu(bs, h, hk):
+    """Causal grids of 16-row halves with more items than CUs (256 on an MI355X) but at most two per CU run
+    rank-major, the heaviest q tile of every sequence first: packed keys and paged caches (block size 256 and
+    96), one and two KV heads, sequences of very different lengths (the short ones' high ranks are empty)."""
+    gen = torch.Generator().manual_seed(81 + (bs or 0) + hk)
+    lens = [333, 150, 271, 500, 9, 310]
+    assert 256 < -(-max(lens) // (64 // (h // hk))) * len(lens) <= 512
+    T = sum(lens)
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32)
+    q = randn(gen, T, h, D)
+    inv = torch.rand(h * D, generator=gen) + 0.5
+    if bs is None:
+        k, v = randn(gen, T, hk, D), randn(gen, T, hk, D)
+        out = varlen_attention(q.to(DEV), k.to(DEV), v.to(DEV), cu_seqlens_q=cu.to(DEV), cu_seqlens_k=cu.to(DEV),
+                               max_seqlen_q=max(lens), softmax_scale=SCALE, causal=True, quant=True,
+                               inv_smooth=inv.to(DEV))
+        want = ref.varlen(q.float(), cu, cu, k=k, v=v)
+    else:
+        kc, vc, tables = paged_pool(gen, lens, sum((n + bs - 1) // bs for n in lens) + 2, block_size=bs, hk=hk)
+        out = paged_prefill_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), tables.to(DEV), cu.to(DEV), cu.to(DEV),
+                                      max(lens), SCALE, quant=True, inv_smooth=inv.to(DEV))
+        want = ref.varlen(q.float(), cu, cu, k_cache=kc, v_cache=vc, block_tables=tables)
+    _check(out, want, f"rank-major int8, block_size {bs}, {h}/{hk} heads", inv)

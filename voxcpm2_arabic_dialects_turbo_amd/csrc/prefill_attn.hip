@@ -644,9 +644,10 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
 template <bool QUANT, int KV, int NW, int RT, int FORM>
 __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 : 2) void prefill_kernel(PrefillArgs p) {
   if constexpr (FORM == kFormRanked) {
-    const int n = p.batch * p.num_kv_heads, id = blockIdx.x, r = id / n, c = (id + r) % n;
+    const int nz = QUANT ? 1 : p.num_kv_heads;  // (QUANT: a workgroup holds every kv head)
+    const int n = p.batch * nz, id = blockIdx.x, r = id / n, c = (id + r) % n;
     const int qt = p.causal ? (int)gridDim.x / n - 1 - r : r;
-    prefill_tile<QUANT, KV, NW, RT>(p, qt, c / p.num_kv_heads, c % p.num_kv_heads);
+    prefill_tile<QUANT, KV, NW, RT>(p, qt, c / nz, c % nz);
   } else if constexpr (FORM == kFormPersistent) {
     constexpr int NTH = 64 * NW * (QUANT ? 2 : 1);
     constexpr int ROWS = 16 * RT * NW;
@@ -877,6 +878,8 @@ hipError_t launch_prefill_int8(const PrefillArgs& a0, int max_seqlen_q, hipStrea
   PrefillArgs a = a0;
   a.xcd_order = (int64_t)q_tiles * a.batch >= kXcdOrderMinWorkgroups;
   const dim3 grid((unsigned)q_tiles, (unsigned)a.batch, 1u);
+  if (r16 && a.causal && grid16 > cus)  // more items than CUs: rank-major, heaviest first
+    return launch_prefill_kind<true, 4, 1, kFormRanked>(a, dim3((unsigned)grid16), stream);
   if (r16) return launch_prefill_kind<true, 4, 1>(a, grid, stream);
   return launch_prefill_kind<true, 4, 2>(a, grid, stream);
 }
