@@ -543,6 +543,41 @@ def bench_kv_copy(dev):
     return out
 
 
+def bench_host_staging(dev, n_req: int = 200, reps: int = 200):
+    """Host-side context staging (runner.py) for a burst of 200 cloned requests, the case the reference times at
+    ~0.4 ms (nanovllm_voxcpm/engine/model_runner.py:851-854, its numpy staging with LoRA contexts, host time):
+    each request a 50-token cached voice prompt plus 46 new tokens in one 256-token block, so the step's context
+    has cu_seqlens, slots and block tables. Host microseconds per prepare_prefill_context call (numpy arrays written
+    into the persistent page-locked staging buffer, one H2D copy queued, context set), and the same for the decode
+    step's prepare_decode_context over the same 200 requests; a persistent StepStaging as the engine keeps."""
+    import time
+
+    import torch
+
+    from voxcpm2_arabic_dialects_turbo_amd import runner
+    from voxcpm2_arabic_dialects_turbo_amd.context import reset_context
+
+    perm = torch.randperm(4 * n_req, generator=torch.Generator().manual_seed(57)).tolist()
+    prefill = [runner.RunnerTask([perm[i]], 96, 50, BS) for i in range(n_req)]
+    decode = [runner.RunnerTask([perm[i]], 97, 96, BS) for i in range(n_req)]
+    staging = runner.StepStaging(dev)
+    out = {}
+    for name, fn, seqs in (("prefill_200_cloned", runner.prepare_prefill_context, prefill),
+                           ("decode_200", runner.prepare_decode_context, decode)):
+        for _ in range(20):
+            fn(seqs, BS, device=dev, staging=staging)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn(seqs, BS, device=dev, staging=staging)
+        host_us = (time.perf_counter() - t0) / reps * 1e6
+        torch.cuda.synchronize()
+        out[name] = dict(host_us=round(host_us, 1))
+    reset_context()
+    out["reference_published_ms"] = {"prefill_200_cloned": 0.4}
+    return out
+
+
 def cpu_config1(budget_s: float = 3.0):
     """Benchmark config 1 on the host cores: the oracle's decode (the reference tests' fp32 _attend over the gathered
     pages) for 1 sequence of context 512, 16 / 2 heads, fp32 caches of 4 blocks x 256 tokens in a random block order,
@@ -692,7 +727,8 @@ def main():
         _progress("prefill legs done")
         line["prefill"]["reference_shapes"] = bench_reference_shapes(dev)
         line["kv_block_prefix_copy"] = bench_kv_copy(dev)
-        _progress("reference shapes and kv copy done")
+        line["host_staging"] = bench_host_staging(dev)
+        _progress("reference shapes, kv copy and host staging done")
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(res["workload"], args.cpu_seconds)
     print(json.dumps(line), flush=True)
