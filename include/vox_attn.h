@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define VOX_ABI_VERSION 6
+#define VOX_ABI_VERSION 7
 
 #define VOX_OK 0
 #define VOX_EINVAL 1 /* bad argument: shape, stride, alignment or null pointer (reference: the asserts of
@@ -117,6 +117,12 @@ size_t vox_prefill_workspace_bytes(int batch);
  *   out_scale[t] = amax / 127,   out_q[t, c] = rint(x[c] / out_scale[t])  (round half to even, int8).
  *   out_q      int8 [T, num_heads * head_dim], token rows out_q_row_stride apart (multiple of 4, 4-byte aligned)
  *   out_scale  fp32 [T]
+ *   num_tokens T, the query rows (cu_seqlens_q[batch], or batch * uniform_seqlen_q)
+ *   workspace  NULL, or >= vox_prefill_int8_workspace_bytes(...) bytes of scratch (16-byte aligned): where that is
+ *              nonzero the call runs as two passes (the bf16 kernel into the workspace, then a per-token
+ *              quantization of its rows), which is faster for long sequences whose work items outnumber the CUs;
+ *              the codes then come from the bf16-rounded o (as the reference's flash-attn + quantize path computes
+ *              them) instead of the fp32 accumulators, within one code step of each other
  * Other arguments as vox_prefill_attn. Supported: num_kv_heads 1 or 2 (one workgroup holds all heads of its tokens). */
 int vox_prefill_attn_int8(const void* q, int64_t q_row_stride, const void* key, const void* value,
                           int64_t key_row_stride, int64_t value_row_stride, const void* k_cache, const void* v_cache,
@@ -124,7 +130,14 @@ int vox_prefill_attn_int8(const void* q, int64_t q_row_stride, const void* key, 
                           int max_blocks, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch,
                           int max_seqlen_q, int uniform_seqlen_q, int uniform_seqlen_k, int num_heads,
                           int num_kv_heads, int head_dim, float softmax_scale, int causal, const float* inv_smooth,
-                          void* out_q, int64_t out_q_row_stride, float* out_scale, void* stream);
+                          void* out_q, int64_t out_q_row_stride, float* out_scale, int64_t num_tokens,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* Scratch bytes for vox_prefill_attn_int8's two-pass form for a call of this shape: num_tokens * num_heads *
+ * head_dim * 2 where the two passes are the faster form, 0 where the fused epilogue is (then pass NULL). No
+ * reference counterpart (the reference's quant kernels allocate their outputs only). */
+size_t vox_prefill_int8_workspace_bytes(int64_t num_tokens, int batch, int max_seqlen_q, int num_heads,
+                                        int num_kv_heads, int head_dim, int causal);
 
 /* Copy the first n token slots of KV-cache blocks in every (layer, K/V) plane, in one launch. Replaces
  * copy_kv_block_prefix (reference: nanovllm_voxcpm/kernels/kv_copy.py:17-41; callers model/runner.py:232-248,

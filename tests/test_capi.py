@@ -126,7 +126,7 @@ def test_prefill_int8_rejects_bad_arguments():
     p = ctypes.c_void_p(256)
     # valid apart from the fake pointers: never passed unmodified (it would launch)
     args = [p, 2048, p, p, 256, 256, None, None, 0, 0, None, 0, 0, p, p, 2, 16, 0, 0, 16, 2, 128, 0.088, 1, None, p,
-            2048, p, None]
+            2048, p, 32, None, 0, None]
     bad = list(args)
     bad[20], bad[19] = 4, 16  # four KV heads: one workgroup would need 1024 threads
     assert lib.vox_prefill_attn_int8(*bad) == _lib.VOX_EINVAL and "num_kv_heads" in _err()
@@ -142,9 +142,39 @@ def test_prefill_int8_rejects_bad_arguments():
     bad = list(args)
     bad[21] = 64  # head_dim, from the shared prefill checks
     assert lib.vox_prefill_attn_int8(*bad) == _lib.VOX_EINVAL and "head_dim" in _err()
+    bad = list(args)
+    bad[28] = -1  # negative num_tokens
+    assert lib.vox_prefill_attn_int8(*bad) == _lib.VOX_EINVAL and "num_tokens" in _err()
+    bad = list(args)
+    bad[13], bad[14], bad[17], bad[18], bad[28] = None, None, 16, 16, 31  # uniform lengths: T must be batch x 16
+    assert lib.vox_prefill_attn_int8(*bad) == _lib.VOX_EINVAL and "num_tokens" in _err()
+    long_ = list(args)  # a shape the two-pass form serves (8 causal sequences of up to 412 tokens)
+    long_[15], long_[16], long_[28] = 8, 412, 2033
+    need = lib.vox_prefill_int8_workspace_bytes(2033, 8, 412, 16, 2, 128, 1)
+    assert need == 2033 * 16 * 128 * 2
+    bad = list(long_)
+    bad[29], bad[30] = p, need - 16  # workspace given but too small: rejected before any launch
+    assert lib.vox_prefill_attn_int8(*bad) == _lib.VOX_EINVAL and "workspace" in _err()
+    bad[29], bad[30] = ctypes.c_void_p(264), need  # not 16-byte aligned
+    assert lib.vox_prefill_attn_int8(*bad) == _lib.VOX_EINVAL and "workspace" in _err()
     zero = list(args)
     zero[15] = 0
     assert lib.vox_prefill_attn_int8(*zero) == _lib.VOX_OK
+
+
+def test_prefill_int8_two_pass_choice():
+    """The int8 output runs as two passes (bf16 attention, then a quantization pass) only for causal calls whose
+    16-row items outnumber the CUs over sequences of 16+ items (the fallback CU count without a GPU is 256); short
+    steps, non-causal rows and rows of more than 2048 values keep the fused epilogue (0 bytes)."""
+    lib = _lib.load()
+    ws = lib.vox_prefill_int8_workspace_bytes
+    assert ws(2033, 8, 412, 16, 2, 128, 1) == 2033 * 16 * 128 * 2  # config 2: 52 tiles x 8 sequences
+    assert ws(2033, 8, 412, 16, 2, 128, 0) == 0                     # non-causal
+    assert ws(2024, 44, 46, 16, 2, 128, 1) == 0                     # 44 x 46: 6 tiles per sequence
+    assert ws(750, 150, 5, 16, 2, 128, 1) == 0                      # LocEnc-sized steps
+    assert ws(600, 2, 300, 16, 2, 128, 1) == 0                      # 76 items: fewer than the CUs
+    assert ws(2033, 8, 412, 32, 2, 128, 1) == 0                     # 4096 values per token row
+    assert ws(0, 8, 412, 16, 2, 128, 1) == 0
 
 
 @pytest.mark.skipif(__import__("torch").cuda.is_available(), reason="launches with placeholder pointers: CPU only")
@@ -157,7 +187,7 @@ def test_prefill_with_one_kv_head_for_128_query_heads_returns_a_status(int8):
     import sys
 
     fn = "vox_prefill_attn_int8" if int8 else "vox_prefill_attn"
-    tail = "None, p, 128 * 128, p, None" if int8 else "p, 128 * 128, None, 0, None"
+    tail = "None, p, 128 * 128, p, 4, None, 0, None" if int8 else "p, 128 * 128, None, 0, None"
     code = f"""
 import ctypes, sys
 sys.path.insert(0, {os.path.dirname(os.path.dirname(os.path.abspath(__file__)))!r})

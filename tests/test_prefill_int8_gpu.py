@@ -17,6 +17,7 @@ import torch
 from oracle import attention as ref
 from tests._util import D, H, HK, paged_pool, randn, uniform_lens
 from tests.golden import make_golden
+from voxcpm2_arabic_dialects_turbo_amd import _lib
 from voxcpm2_arabic_dialects_turbo_amd.kernels.prefill_attn import paged_prefill_attention
 from voxcpm2_arabic_dialects_turbo_amd.kernels.short_attn import short_attention, short_causal_attention
 from voxcpm2_arabic_dialects_turbo_amd.ops import varlen_attention
@@ -167,11 +168,19 @@ def test_int8_sixteen_row_halves_over_several_key_tiles(bs):
     _check(out, want, f"16-row int8, block_size {bs}", inv)
 
 
+@pytest.mark.parametrize("two_pass", [True, False])
 @pytest.mark.parametrize("bs,h,hk", [(None, 16, 2), (256, 16, 2), (96, 16, 2), (None, 8, 1)])
-def test_int8_rank_major_grid_beyond_one_item_per_cu(bs, h, hk):
-    """Causal grids of 16-row halves with more items than CUs (256 on an MI355X) but at most two per CU run
-    rank-major, the heaviest q tile of every sequence first: packed keys and paged caches (block size 256 and
-    96), one and two KV heads, sequences of very different lengths (the short ones' high ranks are empty)."""
+def test_int8_rank_major_grid_beyond_one_item_per_cu(bs, h, hk, two_pass, monkeypatch):
+    """Causal grids of 16-row halves with more items than CUs (256 on an MI355X) over sequences of 16+ items: by
+    default two passes (the bf16 kernel into a scratch buffer, then the per-token quantization); with the library's
+    workspace query forced to 0, the fused epilogue in the rank-major grid, the heaviest q tile of every sequence
+    first. Packed keys and paged caches (block size 256 and 96), one and two KV heads, sequences of very different
+    lengths (the short ones' high ranks are empty)."""
+    lib = _lib.load()
+    # 63 items per sequence x 6 sequences > 256 CUs: the two-pass form unless the query is forced to 0
+    assert lib.vox_prefill_int8_workspace_bytes(sum([333, 150, 271, 500, 9, 310]), 6, 500, h, hk, D, 1) > 0
+    if not two_pass:
+        monkeypatch.setattr(lib, "vox_prefill_int8_workspace_bytes", lambda *a: 0)
     gen = torch.Generator().manual_seed(81 + (bs or 0) + hk)
     lens = [333, 150, 271, 500, 9, 310]
     assert 256 < -(-max(lens) // (64 // (h // hk))) * len(lens) <= 512
@@ -190,4 +199,29 @@ def test_int8_rank_major_grid_beyond_one_item_per_cu(bs, h, hk):
         out = paged_prefill_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), tables.to(DEV), cu.to(DEV), cu.to(DEV),
                                       max(lens), SCALE, quant=True, inv_smooth=inv.to(DEV))
         want = ref.varlen(q.float(), cu, cu, k_cache=kc, v_cache=vc, block_tables=tables)
-    _check(out, want, f"rank-major int8, block_size {bs}, {h}/{hk} heads", inv)
+    _check(out, want, f"rank-major int8, block_size {bs}, {h}/{hk} heads, two passes {two_pass}", inv)
+
+
+def test_int8_two_pass_codes_round_half_to_even_at_exact_ties():
+    """The two-pass form (long causal sequences, more 16-row items than CUs) on exact ties: a zero query gives every
+    visible key the same weight, and each sequence's values are the same at every key position, so o = v exactly
+    (the fp32 sums of half-integers are exact, and o is representable in bf16); with one element 127 per token the
+    scale is exactly 1 and the codes are rint(v), round half to even, bit-exact against the oracle."""
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(79)
+    lens = [400, 390, 380, 370, 360, 350]
+    T = sum(lens)
+    assert lib.vox_prefill_int8_workspace_bytes(T, len(lens), max(lens), H, HK, D, 1) > 0  # the two-pass form
+    ties = torch.tensor([0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5, -3.5, 10.5, -10.5, 126.5, -126.5])
+    t = ties[torch.randint(0, ties.numel(), (len(lens), HK, D), generator=gen)]
+    t[:, 0, 0] = 127.0
+    v = torch.cat([t[b].expand(n, HK, D) for b, n in enumerate(lens)])
+    q, k = torch.zeros(T, H, D, dtype=torch.bfloat16), randn(gen, T, HK, D)
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32)
+    out_q, scale = varlen_attention(q.to(DEV), k.to(DEV), v.to(torch.bfloat16).to(DEV), cu_seqlens_q=cu.to(DEV),
+                                    cu_seqlens_k=cu.to(DEV), max_seqlen_q=max(lens), softmax_scale=SCALE,
+                                    causal=True, quant=True)
+    want = v.repeat_interleave(H // HK, dim=1).reshape(T, H * D)
+    q_ref, s_ref = ref.quantize_rows(want.float())
+    assert torch.equal(scale.cpu(), s_ref) and bool((s_ref == 1.0).all())
+    assert torch.equal(out_q.cpu(), q_ref), "codes differ from round-half-to-even"

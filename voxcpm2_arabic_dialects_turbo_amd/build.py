@@ -21,7 +21,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_NAME = "libvoxattn.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["store_kvcache.hip", "decode_attn.hip", "prefill_attn.hip", "kv_copy.hip", "capi.hip"]
+SOURCES = ["store_kvcache.hip", "decode_attn.hip", "prefill_attn.hip", "quantize_rows.hip", "kv_copy.hip", "capi.hip"]
 PROBE_PATH = os.path.join(PKG_DIR, "libvoxprobe.so")
 PROBE_SOURCES = ["bench_probe.hip"]
 ARCH = "gfx950"

@@ -370,8 +370,10 @@ int vox_prefill_attn_int8(const void* q, int64_t q_row_stride, const void* key, 
                           int max_blocks, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch,
                           int max_seqlen_q, int uniform_seqlen_q, int uniform_seqlen_k, int num_heads,
                           int num_kv_heads, int head_dim, float softmax_scale, int causal, const float* inv_smooth,
-                          void* out_q, int64_t out_q_row_stride, float* out_scale, void* stream) {
-  if (batch < 0 || max_seqlen_q < 0) return fail(VOX_EINVAL, "prefill_attn_int8: negative batch or max_seqlen_q");
+                          void* out_q, int64_t out_q_row_stride, float* out_scale, int64_t num_tokens,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  if (batch < 0 || max_seqlen_q < 0 || num_tokens < 0)
+    return fail(VOX_EINVAL, "prefill_attn_int8: negative batch, max_seqlen_q or num_tokens");
   if (batch == 0 || max_seqlen_q == 0) return VOX_OK;
   if (!out_q || !out_scale) return fail(VOX_EINVAL, "prefill_attn_int8: null out_q or out_scale");
   if (num_kv_heads != 1 && num_kv_heads != 2)
@@ -386,11 +388,37 @@ int vox_prefill_attn_int8(const void* q, int64_t q_row_stride, const void* key, 
                                cu_seqlens_q, cu_seqlens_k, batch, max_seqlen_q, uniform_seqlen_q, uniform_seqlen_k,
                                num_heads, num_kv_heads, head_dim, softmax_scale, causal, &a);
   if (st != VOX_OK) return st;
+  if (!cu_seqlens_q && num_tokens != (int64_t)batch * uniform_seqlen_q)
+    return fail(VOX_EINVAL, "prefill_attn_int8: num_tokens %lld != batch x uniform_seqlen_q", (long long)num_tokens);
+  const size_t need = workspace ? vox_prefill_int8_workspace_bytes(num_tokens, batch, max_seqlen_q, num_heads,
+                                                                   num_kv_heads, head_dim, causal)
+                                : 0;
+  if (need) {
+    // two passes: the bf16 kernel into the workspace ([T, H * 128] bf16), then the per-token quantization
+    if (workspace_bytes < need || !aligned16(workspace))
+      return fail(VOX_EINVAL, "prefill_attn_int8: workspace of %zu bytes (16-byte aligned), %zu needed",
+                  workspace_bytes, need);
+    a.out = (uint16_t*)workspace;
+    a.out_row_stride = (int64_t)num_heads * head_dim;
+    const int st1 = hip_status(vox::launch_prefill(a, max_seqlen_q, (hipStream_t)stream), "prefill_attn_int8 launch");
+    if (st1 != VOX_OK) return st1;
+    return hip_status(vox::launch_quantize_rows((const uint16_t*)workspace, num_tokens, num_heads * head_dim,
+                                                inv_smooth, (int8_t*)out_q, out_q_row_stride, out_scale,
+                                                (hipStream_t)stream),
+                      "prefill_attn_int8 quantization launch");
+  }
   a.inv_smooth = inv_smooth;
   a.out_q = (int8_t*)out_q;
   a.out_row_stride = out_q_row_stride;
   a.out_scale = out_scale;
   return hip_status(vox::launch_prefill_int8(a, max_seqlen_q, (hipStream_t)stream), "prefill_attn_int8 launch");
+}
+
+size_t vox_prefill_int8_workspace_bytes(int64_t num_tokens, int batch, int max_seqlen_q, int num_heads,
+                                        int num_kv_heads, int head_dim, int causal) {
+  if (num_tokens <= 0 || head_dim != kHeadDim || num_heads <= 0 || num_heads * head_dim > 2048) return 0;
+  if (!vox::prefill_int8_two_pass(batch, max_seqlen_q, num_heads, num_kv_heads, causal)) return 0;
+  return (size_t)num_tokens * num_heads * head_dim * 2;
 }
 
 int vox_copy_kv_block_prefix(void* kv, int64_t num_planes, int64_t num_blocks, int block_size,

@@ -861,6 +861,20 @@ hipError_t launch_prefill(const PrefillArgs& a0, int max_seqlen_q, hipStream_t s
   return launch_prefill_kind<false, 4, 2>(a, grid, stream);
 }
 
+// The fused int8 epilogue needs every KV group of a token in one workgroup: two 4-wave halves that share every
+// barrier, 128 KB of LDS, one workgroup per CU, so a CU runs one chain of key tiles where the bf16 kernel runs two
+// workgroups' chains side by side. Where the 16-row halves outnumber the CUs and the sequences span 16+ such
+// tiles (the rank-major int8 grids: long chains, more than one round of workgroups), the bf16 kernel followed by a
+// quantization pass over its rows is faster; short steps keep the fused epilogue (the second launch would cost more
+// than it saves).
+bool prefill_int8_two_pass(int batch, int max_seqlen_q, int num_heads, int num_kv_heads, int causal) {
+  if (batch <= 0 || max_seqlen_q <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return false;
+  const int group = num_heads / num_kv_heads;
+  if (64 % group) return false;
+  const int64_t tiles16 = (max_seqlen_q + 64 / group - 1) / (64 / group);
+  return causal && tiles16 >= 16 && tiles16 * batch > device_cus();
+}
+
 hipError_t launch_prefill_int8(const PrefillArgs& a0, int max_seqlen_q, hipStream_t stream) {
   if (max_seqlen_q <= 0 || a0.batch <= 0) return hipSuccess;
   if (a0.num_kv_heads < 1 || a0.num_kv_heads > 2) return hipErrorInvalidValue;

@@ -103,4 +103,13 @@ hipError_t launch_copy_block_prefix(const CopyArgs& a, int max_tokens, bool vec1
 // The same attention with the int8 epilogue; one workgroup covers every KV group of its tokens (num_kv_heads <= 2).
 hipError_t launch_prefill_int8(const PrefillArgs& a, int max_seqlen_q, hipStream_t stream);
 
+// Whether the int8 output is faster as two passes (the bf16 attention kernel into a scratch buffer, then
+// launch_quantize_rows) than with the fused epilogue, for a call of this shape.
+bool prefill_int8_two_pass(int batch, int max_seqlen_q, int num_heads, int num_kv_heads, int causal);
+
+// Per-token int8 quantization of `rows` bf16 rows of `row_elems` values (contiguous, row_elems a multiple of 8,
+// at most 2048): out_q[t] = rint(x[t] * inv_smooth / scale_t), out_scale[t] = scale_t = max(amax_t, 1e-6) / 127.
+hipError_t launch_quantize_rows(const uint16_t* x, int64_t rows, int row_elems, const float* inv_smooth, int8_t* out_q,
+                                int64_t out_row_stride, float* out_scale, hipStream_t stream);
+
 }  // namespace vox

@@ -197,13 +197,18 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor | None, v: torch.Tensor | 
     if H % HK:
         raise ValueError(f"num_heads {H} is not a multiple of num_kv_heads {HK}")
     if quant:
+        # long sequences whose work items outnumber the CUs run as two passes (bf16 attention into a scratch buffer,
+        # then the per-token quantization): the library sizes the scratch, 0 where the fused epilogue is faster
+        ws_bytes = lib.vox_prefill_int8_workspace_bytes(T, B, int(max_seqlen_q), H, HK, D, 1 if causal else 0)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
         _lib.check(lib.vox_prefill_attn_int8(q.data_ptr(), q.stride(0), *args,
                                              None if cu_q is None else cu_q.data_ptr(),
                                              None if cu_k is None else cu_k.data_ptr(), B, int(max_seqlen_q),
                                              int(uniform_seqlen_q), int(uniform_seqlen_k), H, HK, D,
                                              float(softmax_scale), 1 if causal else 0,
                                              None if inv_smooth is None else inv_smooth.data_ptr(),
-                                             out_q.data_ptr(), out_q.stride(0), out_scale.data_ptr(),
+                                             out_q.data_ptr(), out_q.stride(0), out_scale.data_ptr(), T,
+                                             None if ws is None else ws.data_ptr(), ws_bytes,
                                              _lib.stream_handle(dev)),
                    "prefill_attn_int8")
         return out
