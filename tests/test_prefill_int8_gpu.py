@@ -225,3 +225,19 @@ def test_int8_two_pass_codes_round_half_to_even_at_exact_ties():
     q_ref, s_ref = ref.quantize_rows(want.float())
     assert torch.equal(scale.cpu(), s_ref) and bool((s_ref == 1.0).all())
     assert torch.equal(out_q.cpu(), q_ref), "codes differ from round-half-to-even"
+
+
+def test_int8_two_pass_with_uniform_lengths():
+    """The two-pass form without cu_seqlens (batch x uniform lengths, the flash_attn_func layout): 6 causal
+    sequences of 400 tokens, token count batch x 400, against the oracle with inv_smooth."""
+    lib = _lib.load()
+    B, L = 6, 400
+    assert lib.vox_prefill_int8_workspace_bytes(B * L, B, L, H, HK, D, 1) > 0
+    gen = torch.Generator().manual_seed(82)
+    q, k, v = randn(gen, B * L, H, D), randn(gen, B * L, HK, D), randn(gen, B * L, HK, D)
+    inv = torch.rand(H * D, generator=gen) + 0.5
+    out = varlen_attention(q.to(DEV), k.to(DEV), v.to(DEV), cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q=L,
+                           batch=B, uniform_seqlen_q=L, uniform_seqlen_k=L, softmax_scale=SCALE, causal=True,
+                           quant=True, inv_smooth=inv.to(DEV))
+    cu = torch.arange(0, B * L + 1, L, dtype=torch.int32)
+    _check(out, ref.varlen(q.float(), cu, cu, k=k, v=v), "uniform two-pass int8", inv)
