@@ -8,8 +8,9 @@
 // reference's unfused path applies to flash-attn's bf16 output the same way).
 //
 // One wave per row: lane l takes the 16-byte chunks l, l + 64, ... of the row (8 values each, coalesced), the row max
-// is a wave reduction, and each chunk leaves as 8 int8 codes in one 8-byte store. HBM-bound and short; the rows are
-// the attention pass's output, still in L2 / the Infinity Cache when this pass runs next on the stream.
+// is a wave reduction (DPP and lane swaps, no LDS), and each chunk leaves as 8 int8 codes in one 8-byte store. Short
+// and latency-bound (one load round trip, a reduction, the stores); the rows are the attention pass's output, which
+// runs just before it on the stream.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -52,8 +53,7 @@ __global__ __launch_bounds__(64 * kQWaves) void quantize_rows_kernel(const uint1
       for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[i][e]));
     }
   }
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, kWave));
+  amax = wave_max(amax);
   const float scale = fmaxf(amax, 1e-6f) / 127.f;
   // rint(x / scale) without a division per element, as in the fused epilogue: y = x * (1 / scale) is within 2.5e-5 of
   // the quotient (|x / scale| <= 127.5, two roundings), so rint(y) is the same code unless y lies within 1e-4 of a

@@ -69,6 +69,16 @@ __device__ __forceinline__ float xrow_sum(float x) {
 __device__ __forceinline__ float col_max4(float x) { return xrow_max(xhalf_max(x)); }
 __device__ __forceinline__ float col_sum4(float x) { return xrow_sum(xhalf_sum(x)); }
 
+// Max over the 64 lanes of a wavefront: row_ror DPP steps (8, 4, 2, 1) within each 16-lane row, then the four rows
+// through col_max4. No LDS (the __shfl_xor form goes through ds_bpermute, one LDS round trip per step).
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false)));
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xF, 0xF, false)));
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x122, 0xF, 0xF, false)));
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x121, 0xF, 0xF, false)));
+  return col_max4(x);
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Inclusive prefix sum over the 64 lanes of a wavefront.
