@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define VOX_ABI_VERSION 7
+#define VOX_ABI_VERSION 8
 
 #define VOX_OK 0
 #define VOX_EINVAL 1 /* bad argument: shape, stride, alignment or null pointer (reference: the asserts of
@@ -56,6 +56,24 @@ int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, co
                     int max_blocks, const int32_t* context_lens, int batch, int num_heads, int num_kv_heads,
                     int head_dim, float softmax_scale, void* workspace, size_t workspace_bytes, void* out,
                     void* stream);
+
+/* The decode step's KV store and decode attention in one call: vox_store_kvcache(key, value, key_row_stride,
+ * value_row_stride, k_cache, v_cache, num_blocks * block_size, slot_mapping, batch, ...) followed by
+ * vox_decode_attn(...) (reference: the decode branch of nanovllm_voxcpm/model/layers.py:326-358, store_kvcache then
+ * flash_attn_with_kvcache), without the store's own launch: the split kernel reads each sequence's new token from
+ * key / value where the tile it loads holds that token's slot, and the merge kernel writes the rows into the caches
+ * after every read. Same results as the two calls when no slot_mapping[b] lies inside another sequence's context
+ * (the engine's sequences each write only their own last block); slot -1 and slots outside the cache store nothing.
+ *   key / value    bf16 [batch, num_kv_heads, head_dim], heads contiguous, rows *_row_stride elements apart
+ *                  (multiples of 8), 16-byte aligned
+ *   slot_mapping   int32 [batch]
+ * Other arguments as vox_decode_attn. */
+int vox_decode_attn_store(const void* q, int64_t q_row_stride, const void* key, const void* value,
+                          int64_t key_row_stride, int64_t value_row_stride, const int32_t* slot_mapping,
+                          void* k_cache, void* v_cache, int64_t num_blocks, int block_size,
+                          const int32_t* block_tables, int64_t bt_stride, int max_blocks, const int32_t* context_lens,
+                          int batch, int num_heads, int num_kv_heads, int head_dim, float softmax_scale,
+                          void* workspace, size_t workspace_bytes, void* out, void* stream);
 
 /* vox_decode_attn without the workspace argument: the split-KV scratch is a static device array of 16 MiB
  * (16777216 bytes) that each GPU the library runs on holds until the process ends, so the

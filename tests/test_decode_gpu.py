@@ -237,3 +237,90 @@ def test_unmapped_blocks_inside_the_context_are_masked_like_prefill():
     pre = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), cu_q, cu_k, 1, max(lens), softmax_scale=SCALE,
                                  causal=True, block_table=bad.to(DEV))
     attn_close(pre, out.float(), "prefill nq=1 vs decode on the same unmapped blocks")
+
+
+def _store_then_decode(q, key, value, slots, kc, vc, lens, tables):
+    """The two-call reference of the store mode: store_kvcache, then decode, on copies of the caches."""
+    from voxcpm2_arabic_dialects_turbo_amd.ops import store_kvcache
+
+    k2, v2 = kc.clone(), vc.clone()
+    store_kvcache(key, value, k2, v2, slots)
+    return decode_attention(q, k2, v2, lens, tables, SCALE), k2, v2
+
+
+@pytest.mark.parametrize("case", ["last_token", "middle_slot", "one_kv_head", "wide_table", "two_launches"])
+def test_decode_with_the_store_matches_store_then_decode(case):
+    """The decode call with the step's store folded in (vox_decode_attn_store) against store_kvcache followed by
+    decode_attention: outputs and caches bit-identical. The new token at each sequence's last position (the
+    engine's layout), or at a slot in the middle of its own context; padded rows (context 0, slot -1); one KV head;
+    a block table too wide for LDS; more sequences than one launch takes. Key / value rows are strided views of a
+    fused qkv row, as the model hands them over."""
+    gen = torch.Generator().manual_seed(91)
+    hk = 1 if case == "one_kv_head" else HK
+    h = 8 if case == "one_kv_head" else H
+    B = {"wide_table": 512, "two_launches": 600}.get(case, 150)
+    lens = uniform_lens(gen, B, 1, {"two_launches": 700, "wide_table": 600}.get(case, 2048))
+    lens[3] = 0  # a padded row
+    bs = 256 if case != "wide_table" else 32
+    kc, vc, tables = paged_pool(gen, lens, sum(-(-max(n, 1) // bs) for n in lens) + 4, block_size=bs, hk=hk)
+    qkv = randn(gen, B, (h + 2 * hk) * D).to(DEV)
+    q, key, value = qkv.split([h * D, hk * D, hk * D], dim=-1)
+    q, key, value = q.view(B, h, D), key.view(B, hk, D), value.view(B, hk, D)
+    slots = []
+    for b, n in enumerate(lens):
+        if n == 0:
+            slots.append(-1)
+            continue
+        pos = n - 1 if case != "middle_slot" else (n - 1) // 2
+        slots.append(int(tables[b, pos // bs]) * bs + pos % bs)
+    slots = torch.tensor(slots, dtype=torch.int32, device=DEV)
+    kc, vc, tables = kc.to(DEV), vc.to(DEV), tables.to(DEV)
+    lens_d = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    want, k_want, v_want = _store_then_decode(q, key, value, slots, kc, vc, lens_d, tables)
+    k1, v1 = kc.clone(), vc.clone()
+    got = decode_attention(q, k1, v1, lens_d, tables, SCALE, key=key, value=value, slot_mapping=slots)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), f"{case}: outputs differ from store + decode"
+    assert torch.equal(k1, k_want) and torch.equal(v1, v_want), f"{case}: caches differ from store_kvcache's"
+
+
+def test_decode_with_the_store_in_a_hip_graph_replays_like_eager():
+    """Store mode captured in a HIP graph and replayed over changing inputs (new tokens, positions and slots
+    written into the captured buffers), each replay against the two-call form run eagerly."""
+    gen = torch.Generator().manual_seed(92)
+    B, pool = 64, 600
+    lens = uniform_lens(gen, B, 100, 1500)
+    kc, vc, tables_h = paged_pool(gen, [n + 8 for n in lens], pool)
+    kc, vc, tables = kc.to(DEV), vc.to(DEV), tables_h.to(DEV)
+    q = torch.zeros(B, H, D, dtype=torch.bfloat16, device=DEV)
+    key = torch.zeros(B, HK, D, dtype=torch.bfloat16, device=DEV)
+    value = torch.zeros_like(key)
+    lens_d = torch.zeros(B, dtype=torch.int32, device=DEV)
+    slots = torch.zeros(B, dtype=torch.int32, device=DEV)
+    out = torch.empty(B, H, D, dtype=torch.bfloat16, device=DEV)
+    k1, v1 = kc.clone(), vc.clone()
+
+    def load(step):
+        n = torch.tensor([x + step for x in lens], dtype=torch.int32)
+        s = torch.tensor([int(tables_h[b, (int(n[b]) - 1) // BLOCK]) * BLOCK + (int(n[b]) - 1) % BLOCK
+                          for b in range(B)], dtype=torch.int32)
+        q.copy_(randn(gen, B, H, D))
+        key.copy_(randn(gen, B, HK, D))
+        value.copy_(randn(gen, B, HK, D))
+        lens_d.copy_(n)
+        slots.copy_(s)
+
+    load(0)
+    decode_attention(q, k1, v1, lens_d, tables, SCALE, out=out, key=key, value=value, slot_mapping=slots)
+    k_ref, v_ref = k1.clone(), v1.clone()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        decode_attention(q, k1, v1, lens_d, tables, SCALE, out=out, key=key, value=value, slot_mapping=slots)
+    for step in range(1, 5):
+        load(step)
+        want, k_ref, v_ref = _store_then_decode(q, key, value, slots, k_ref, v_ref, lens_d, tables)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {step}: output"
+        assert torch.equal(k1, k_ref) and torch.equal(v1, v_ref), f"replay {step}: caches"

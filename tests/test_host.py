@@ -162,13 +162,14 @@ def test_decode_graph_buffers_load_like_run_model():
 class _Recorder:
     def __init__(self, monkeypatch):
         self.calls = []
-        for name in ("store_kvcache", "flash_attn_varlen_func", "flash_attn_with_kvcache", "flash_attn_func"):
+        for name in ("store_kvcache", "flash_attn_varlen_func", "flash_attn_with_kvcache", "flash_attn_func",
+                     "decode_attention"):
             monkeypatch.setattr(layers, name, self._make(name))
 
     def _make(self, name):
         def fn(*args, **kwargs):
             self.calls.append((name, args, kwargs))
-            return "o"
+            return torch.zeros(args[0].shape) if name == "decode_attention" else "o"
         return fn
 
 
@@ -209,16 +210,32 @@ def test_warmup_prefill_without_caches_skips_the_store(monkeypatch):
     assert [c[0] for c in rec.calls] == ["flash_attn_varlen_func"]
 
 
-def test_decode_calls_the_kvcache_kernel_with_an_unsqueezed_query(monkeypatch):
+def test_decode_stores_and_attends_in_one_call_with_an_unsqueezed_output(monkeypatch):
+    """A decode step with caches: the store rides in the decode call (key / value / slot_mapping of the step), the
+    output comes back [B, 1, H, D] as flash_attn_with_kvcache's does."""
     rec = _Recorder(monkeypatch)
     attn = Attention(16, 128, 0.125, 2)
     attn.k_cache, attn.v_cache = torch.zeros(2, 256, 2, 128), torch.zeros(2, 256, 2, 128)
     lens, bt = torch.tensor([7, 9], dtype=torch.int32), torch.tensor([[0], [1]], dtype=torch.int32)
+    slots = torch.tensor([6, 264], dtype=torch.int32)
+    set_context(False, slot_mapping=slots, context_lens=lens, block_tables=bt)
+    q, k, v = torch.zeros(2, 16, 128), torch.zeros(2, 2, 128), torch.zeros(2, 2, 128)
+    o = attn(q, k, v)
+    [(n0, a0, kw0)] = rec.calls
+    assert n0 == "decode_attention" and a0[0] is q and a0[1] is attn.k_cache and a0[2] is attn.v_cache
+    assert a0[3] is lens and a0[4] is bt and a0[5] == 0.125
+    assert kw0["key"] is k and kw0["value"] is v and kw0["slot_mapping"] is slots
+    assert o.shape == (2, 1, 16, 128)
+
+
+def test_decode_without_caches_calls_the_kvcache_kernel_with_an_unsqueezed_query(monkeypatch):
+    rec = _Recorder(monkeypatch)
+    attn = Attention(16, 128, 0.125, 2)
+    lens, bt = torch.tensor([7, 9], dtype=torch.int32), torch.tensor([[0], [1]], dtype=torch.int32)
     set_context(False, slot_mapping=torch.tensor([6, 264], dtype=torch.int32), context_lens=lens, block_tables=bt)
     attn(torch.zeros(2, 16, 128), torch.zeros(2, 2, 128), torch.zeros(2, 2, 128))
-    (n0, _, _), (n1, a1, kw1) = rec.calls
-    assert n0 == "store_kvcache" and n1 == "flash_attn_with_kvcache"
-    assert a1[0].shape == (2, 1, 16, 128) and a1[1] is attn.k_cache
+    [(n1, a1, kw1)] = rec.calls
+    assert n1 == "flash_attn_with_kvcache" and a1[0].shape == (2, 1, 16, 128)
     assert kw1 == dict(cache_seqlens=lens, block_table=bt, softmax_scale=0.125, causal=True)
 
 

@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must be loaded before the library: shared HIP runti
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvoxattn.so")
 
 VOX_OK, VOX_EINVAL, VOX_EHIP = 0, 1, 2
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # every symbol include/vox_attn.h declares
 EXPORTS = (
@@ -25,6 +25,7 @@ EXPORTS = (
     "vox_abi_version",
     "vox_store_kvcache",
     "vox_decode_attn",
+    "vox_decode_attn_store",
     "vox_decode_attn_noalloc",
     "vox_decode_workspace_bytes",
     "vox_decode_workgroups",
@@ -45,6 +46,9 @@ _SIGNATURES = {
                                  _i32, _i32, _c_void_p]),
     "vox_decode_attn": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _i64, _i32,
                                _c_void_p, _i32, _i32, _i32, _i32, _f32, _c_void_p, _size, _c_void_p, _c_void_p]),
+    "vox_decode_attn_store": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p,
+                                     _c_void_p, _i64, _i32, _c_void_p, _i64, _i32, _c_void_p, _i32, _i32, _i32, _i32,
+                                     _f32, _c_void_p, _size, _c_void_p, _c_void_p]),
     "vox_decode_attn_noalloc": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _i64, _i32,
                                        _c_void_p, _i32, _i32, _i32, _i32, _f32, _c_void_p, _c_void_p]),
     "vox_decode_workspace_bytes": (_size, [_i32]),

@@ -113,6 +113,11 @@ int launch_decode_slices(const vox::DecodeArgs& a, int batch, int num_kv_heads, 
       s.q = base.q + (int64_t)b0 * base.q_row_stride;
       s.context_lens = base.context_lens + b0;
       s.out = base.out + (int64_t)b0 * base.out_row_stride;
+      if (base.slot_mapping) {
+        s.slot_mapping = base.slot_mapping + b0;
+        s.new_k = base.new_k + (int64_t)b0 * base.new_k_stride;
+        s.new_v = base.new_v + (int64_t)b0 * base.new_v_stride;
+      }
     }
     const int st = hip_status(vox::launch_decode(s, num_kv_heads, stream), "decode launch");
     if (st != VOX_OK) return st;
@@ -123,13 +128,14 @@ int launch_decode_slices(const vox::DecodeArgs& a, int batch, int num_kv_heads, 
 
 extern "C" {
 
-int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
-                    int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
-                    int max_blocks, const int32_t* context_lens, int batch, int num_heads, int num_kv_heads,
-                    int head_dim, float softmax_scale, void* workspace, size_t workspace_bytes, void* out,
-                    void* stream) {
-  if (batch < 0) return fail(VOX_EINVAL, "decode_attn: batch < 0");
-  if (batch == 0) return VOX_OK;
+}  // extern "C"
+
+namespace {
+// Validates a decode call's arguments (batch > 0) and fills its launch descriptor.
+int decode_setup(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache, int64_t num_blocks,
+                 int block_size, const int32_t* block_tables, int64_t bt_stride, int max_blocks,
+                 const int32_t* context_lens, int batch, int num_heads, int num_kv_heads, int head_dim,
+                 float softmax_scale, void* workspace, size_t workspace_bytes, void* out, vox::DecodeArgs* out_args) {
   if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out)
     return fail(VOX_EINVAL, "decode_attn: null pointer argument");
   if (head_dim != kHeadDim) return fail(VOX_EINVAL, "decode_attn: head_dim %d unsupported (128 only)", head_dim);
@@ -152,7 +158,8 @@ int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, co
   if (workspace_bytes < need || !workspace)
     return fail(VOX_EINVAL, "decode_attn: workspace of %zu bytes, %zu needed", workspace_bytes, need);
 
-  vox::DecodeArgs a{};
+  vox::DecodeArgs& a = *out_args;
+  a = vox::DecodeArgs{};
   a.q = (const uint16_t*)q;
   a.q_row_stride = q_row_stride;
   a.k_cache = (const uint16_t*)k_cache;
@@ -170,7 +177,52 @@ int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, co
   a.grid = grid;
   a.out = (uint16_t*)out;
   a.out_row_stride = (int64_t)num_heads * head_dim;
+  return VOX_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
+                    int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
+                    int max_blocks, const int32_t* context_lens, int batch, int num_heads, int num_kv_heads,
+                    int head_dim, float softmax_scale, void* workspace, size_t workspace_bytes, void* out,
+                    void* stream) {
+  if (batch < 0) return fail(VOX_EINVAL, "decode_attn: batch < 0");
+  if (batch == 0) return VOX_OK;
+  vox::DecodeArgs a;
+  const int st = decode_setup(q, q_row_stride, k_cache, v_cache, num_blocks, block_size, block_tables, bt_stride,
+                              max_blocks, context_lens, batch, num_heads, num_kv_heads, head_dim, softmax_scale,
+                              workspace, workspace_bytes, out, &a);
+  if (st != VOX_OK) return st;
   // batches beyond one launch's LDS step layout run as consecutive launches on the stream (shared workspace)
+  return launch_decode_slices(a, batch, num_kv_heads, workspace, (hipStream_t)stream);
+}
+
+int vox_decode_attn_store(const void* q, int64_t q_row_stride, const void* key, const void* value,
+                          int64_t key_row_stride, int64_t value_row_stride, const int32_t* slot_mapping,
+                          void* k_cache, void* v_cache, int64_t num_blocks, int block_size,
+                          const int32_t* block_tables, int64_t bt_stride, int max_blocks, const int32_t* context_lens,
+                          int batch, int num_heads, int num_kv_heads, int head_dim, float softmax_scale,
+                          void* workspace, size_t workspace_bytes, void* out, void* stream) {
+  if (batch < 0) return fail(VOX_EINVAL, "decode_attn_store: batch < 0");
+  if (batch == 0) return VOX_OK;
+  if (!key || !value || !slot_mapping) return fail(VOX_EINVAL, "decode_attn_store: null key, value or slot_mapping");
+  const int64_t row = (int64_t)num_kv_heads * head_dim;
+  if (key_row_stride < row || value_row_stride < row || key_row_stride % 8 || value_row_stride % 8 ||
+      !aligned16(key) || !aligned16(value))
+    return fail(VOX_EINVAL, "decode_attn_store: key / value rows must be 16-byte aligned, strides multiples of 8 "
+                            "elements and at least num_kv_heads * head_dim");
+  vox::DecodeArgs a;
+  const int st = decode_setup(q, q_row_stride, k_cache, v_cache, num_blocks, block_size, block_tables, bt_stride,
+                              max_blocks, context_lens, batch, num_heads, num_kv_heads, head_dim, softmax_scale,
+                              workspace, workspace_bytes, out, &a);
+  if (st != VOX_OK) return st;
+  a.slot_mapping = slot_mapping;
+  a.new_k = (const uint16_t*)key;
+  a.new_v = (const uint16_t*)value;
+  a.new_k_stride = key_row_stride;
+  a.new_v_stride = value_row_stride;
   return launch_decode_slices(a, batch, num_kv_heads, workspace, (hipStream_t)stream);
 }
 

@@ -89,6 +89,28 @@ __device__ __forceinline__ void load_tile(Tile<HK>& T, const DecodeArgs& p, int6
   for (int i = 0; i < TT::VP; ++i) T.v[i] = ld_g16(vb + i * 1024);
 }
 
+// load_tile in store mode: tile row r_new (-1: none) is the step's new token, read from its K / V rows nk / nv
+// instead of the cache (the same loads, with the lanes of that row pointed at the new row: no extra load).
+template <int HK>
+__device__ __forceinline__ void load_tile_new(Tile<HK>& T, const DecodeArgs& p, int64_t slot0, uint32_t koff,
+                                              uint32_t voff, int r_new, const uint16_t* nk, const uint16_t* nv) {
+  using TT = Tile<HK>;
+  const int lane = threadIdx.x & 63;
+  const char* kb = reinterpret_cast<const char*>(p.k_cache + slot0 * TT::ROW) + koff;
+  const char* vb = reinterpret_cast<const char*>(p.v_cache + slot0 * TT::ROW) + voff;
+  // K: lane (row r16, dims jq * 8 + ...): the new row's same dims, at koff less the row offset
+  if ((lane & 15) == r_new) kb = reinterpret_cast<const char*>(nk) + (koff - (uint32_t)(r_new * TT::ROW) * 2u);
+#pragma unroll
+  for (int kc = 0; kc < TT::KC; ++kc) T.k[kc] = ld_g16(kb + kc * 64);
+  // V piece i holds slot row i * 64 / PPR + lane / PPR, dims (lane % PPR) * 8
+  const char* nvb = reinterpret_cast<const char*>(nv) + (uint32_t)((lane % TT::PPR) * 8) * 2u;
+#pragma unroll
+  for (int i = 0; i < TT::VP; ++i) {
+    const bool mine = i * (64 / TT::PPR) + lane / TT::PPR == r_new;
+    T.v[i] = ld_g16(mine ? nvb : vb + i * 1024);
+  }
+}
+
 // floor((a * b + c) / d) for the step-range bounds (all operands >= 0, d > 0): one 32-bit division when the
 // numerator fits in 32 bits, as it does for every real step, instead of the long 64-bit sequence.
 __device__ __forceinline__ int64_t muldiv(int64_t a, int64_t b, int64_t c, int64_t d) {
@@ -125,6 +147,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   __shared__ __attribute__((aligned(16))) float s_slot[kSlots * kPartialFloats];  // (wave, segment) partials
   __shared__ int s_ctx[kMaxSeqPerLaunch];        // context per sequence, cut to the table's reach
   __shared__ int s_row[kMaxSeqPerLaunch];        // q / output row per sequence
+  __shared__ int s_snew[kMaxSeqPerLaunch];       // store mode: the cache slot of each sequence's new token
   __shared__ int s_start[kMaxSeqPerLaunch + 1];  // first step per sequence; s_start[batch] = total steps
   __shared__ int s_wtot[kWaves];
   __shared__ int s_wmax[kWaves];  // most steps of one sequence, per wave
@@ -204,6 +227,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
     }
     if (bb < p.batch) {
       s_ctx[bb] = ctx;
+      if (p.slot_mapping) s_snew[bb] = p.slot_mapping[bb];
       s_row[bb] = row;
       s_start[bb] = run + before + incl - n;
     }
@@ -261,7 +285,17 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   auto issue = [&](Tile<HK>& T, int64_t blk, int bs, int t) {  // loads of range tile t (sequence bs), block blk
     T.ok = blk >= 0 && blk < p.num_blocks;
     const int tok = (t - start_of(bs)) * kTile;
-    load_tile<HK>(T, p, (T.ok ? blk : 0) * p.block_size + (tok % p.block_size), koff, voff);
+    const int64_t slot0 = (T.ok ? blk : 0) * p.block_size + (tok % p.block_size);
+    if (!p.slot_mapping) {
+      load_tile<HK>(T, p, slot0, koff, voff);
+      return;
+    }
+    // store mode: the tile holds the new token when its slot lies in [slot0, slot0 + 16) (unmapped tiles are masked
+    // whatever they read)
+    const int64_t dn = (int64_t)uniform(s_snew[bs]) - slot0;
+    const int r_new = dn >= 0 && dn < kTile ? (int)dn : -1;
+    load_tile_new<HK>(T, p, slot0, koff, voff, r_new, p.new_k + (int64_t)bs * p.new_k_stride,
+                      p.new_v + (int64_t)bs * p.new_v_stride);
   };
   auto load_q = [&](u32x4 (&qv)[4], int bs) {  // query row of head r16: d = kq*32 + jq*8 + [0, 8)
     const uint16_t* qb = p.q + (int64_t)uniform(s_row[bs]) * p.q_row_stride + (int64_t)(h < H ? h : 0) * kD + jq * 8;
@@ -499,6 +533,17 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs p) {
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
+  if (p.slot_mapping) {  // store mode: the new K / V row into the cache, now that every read of the split is done
+    const int row_elems = p.group ? p.num_heads / p.group * kD : 0;  // HK x 128
+    const int64_t slot = p.slot_mapping[b];
+    const int chunk = tid & 127;  // 16-byte chunk of the row: threads 0-127 K, 128-255 V
+    if (slot >= 0 && slot < p.num_blocks * p.block_size && chunk * 8 < row_elems) {
+      const bool is_v = tid >= 128;
+      const uint16_t* src = (is_v ? p.new_v + (int64_t)b * p.new_v_stride : p.new_k + (int64_t)b * p.new_k_stride);
+      uint16_t* dst = const_cast<uint16_t*>(is_v ? p.v_cache : p.k_cache) + slot * row_elems;
+      *reinterpret_cast<u32x4*>(dst + chunk * 8) = ld_g16(src + chunk * 8);
+    }
+  }
   const int hh = tid >> 4;
   const int d0 = (tid & 15) * 8;
   const int H = p.num_heads;

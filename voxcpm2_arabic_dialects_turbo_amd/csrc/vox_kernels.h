@@ -38,6 +38,16 @@ struct DecodeArgs {
   // of its table row, and its q and output row is cu_q[b]. Every other sequence is left alone: no keys, no output.
   const int32_t* cu_q;
   const int32_t* cu_k;
+  // Store mode (slot_mapping != nullptr; not with cu_q): this step's K/V row of every sequence, bf16 [B, HK, 128]
+  // with heads contiguous and rows new_*_stride elements apart, belongs at cache slot slot_mapping[b] (-1 = none).
+  // The split kernel reads that slot's token from the row instead of the cache (a tile holding the slot takes the
+  // row's K and V there), and the merge kernel writes the rows into the cache after every read: the result is that
+  // of storing first and then attending, as long as no sequence's slot lies inside another sequence's context.
+  const int32_t* slot_mapping;
+  const uint16_t* new_k;
+  const uint16_t* new_v;
+  int64_t new_k_stride;
+  int64_t new_v_stride;
 };
 
 struct PrefillArgs {

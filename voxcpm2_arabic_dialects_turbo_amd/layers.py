@@ -6,7 +6,8 @@
 ``forward(q, k, v)`` dispatch, reading the forward context at call time
 (reference: nanovllm_voxcpm/model/layers.py:308-362):
 
-- causal, caches allocated: store this step's K/V at ``slot_mapping`` first;
+- causal, caches allocated: store this step's K/V at ``slot_mapping`` first (in a decode step, inside the decode
+  call itself: the same result without the store's own launch);
 - causal prefill: varlen attention over the step's own k / v, or over the caches when ``block_tables`` is set
   (prefix cache, mixed prefill + decode steps, prefill graphs), bottom-right causal;
 - causal decode: paged split-KV decode over ``context_lens`` / ``block_tables``; returns [B, 1, H, D];
@@ -22,7 +23,7 @@ import torch
 from torch import nn
 
 from .context import get_context
-from .ops import flash_attn_func, flash_attn_varlen_func, flash_attn_with_kvcache, store_kvcache
+from .ops import decode_attention, flash_attn_func, flash_attn_varlen_func, flash_attn_with_kvcache, store_kvcache
 
 __all__ = ["Attention", "store_kvcache"]
 
@@ -49,7 +50,14 @@ class Attention(nn.Module):
         if self.is_causal:
             context = get_context()
             k_cache, v_cache = self.k_cache, self.v_cache
-            if k_cache.numel() and v_cache.numel():
+            cached = bool(k_cache.numel() and v_cache.numel())
+            if cached and not context.is_prefill and context.slot_mapping is not None and k.dim() == 3 \
+                    and k.shape[0] == q.shape[0]:
+                # decode step: the store rides in the decode call (one row per sequence, each writing the slot of
+                # its own newest token)
+                return decode_attention(q, k_cache, v_cache, context.context_lens, context.block_tables, self.scale,
+                                        key=k, value=v, slot_mapping=context.slot_mapping).unsqueeze(1)
+            if cached:
                 store_kvcache(k, v, k_cache, v_cache, context.slot_mapping)
             if context.is_prefill:
                 if context.block_tables is not None:  # prefix cache: keys through the block tables

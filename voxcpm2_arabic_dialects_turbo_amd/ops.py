@@ -78,11 +78,17 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
 
 
 def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, context_lens: torch.Tensor,
-                     block_tables: torch.Tensor, softmax_scale: float, out: torch.Tensor | None = None
-                     ) -> torch.Tensor:
+                     block_tables: torch.Tensor, softmax_scale: float, out: torch.Tensor | None = None,
+                     key: torch.Tensor | None = None, value: torch.Tensor | None = None,
+                     slot_mapping: torch.Tensor | None = None) -> torch.Tensor:
     """One query token per sequence: q [B, H, 128] (sequence rows may be strided) over the paged cache
     [num_blocks, block_size, HK, 128] through block_tables int32 [B, max_blocks]; context_lens int32 [B].
-    Returns o [B, H, 128] bf16 (contiguous). Rows with context_lens == 0 get zeros."""
+    Returns o [B, H, 128] bf16 (contiguous). Rows with context_lens == 0 get zeros.
+
+    With key / value ([B, HK, 128], rows may be strided) and slot_mapping ([B]), the decode step's KV store happens
+    in the same call: the result (and the caches afterwards) are those of store_kvcache(key, value, k_cache,
+    v_cache, slot_mapping) followed by this attention, as long as no sequence's slot lies inside another
+    sequence's context (the engine's decode steps: each sequence writes its own last block)."""
     B, H, D = q.shape
     dev = _check_cuda(q, k_cache, v_cache, context_lens, block_tables)
     if q.dtype != torch.bfloat16 or k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
@@ -113,11 +119,29 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     lib = _lib.load()
     ws_bytes = lib.vox_decode_workspace_bytes(B)
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
-    _lib.check(lib.vox_decode_attn(q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), num_blocks,
-                                   block_size, bt.data_ptr(), bt.stride(0), max_blocks, lens.data_ptr(), B, H, HK, D,
-                                   float(softmax_scale), ws.data_ptr(), ws.numel(), out.data_ptr(),
-                                   _lib.stream_handle(dev)),
-               "decode_attn")
+    if key is None:
+        _lib.check(lib.vox_decode_attn(q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), num_blocks,
+                                       block_size, bt.data_ptr(), bt.stride(0), max_blocks, lens.data_ptr(), B, H, HK,
+                                       D, float(softmax_scale), ws.data_ptr(), ws.numel(), out.data_ptr(),
+                                       _lib.stream_handle(dev)),
+                   "decode_attn")
+        return out
+    _check_cuda(q, key, value, slot_mapping)
+    if key.dtype != k_cache.dtype or value.dtype != v_cache.dtype:
+        raise TypeError(f"decode store: key/value dtype {key.dtype}/{value.dtype} differs from the caches'")
+    if key.shape != (B, HK, D) or value.shape != (B, HK, D):
+        raise ValueError(f"decode store: key and value must be [{B}, {HK}, {D}], got {tuple(key.shape)}")
+    if key.stride(2) != 1 or key.stride(1) != D or value.stride(2) != 1 or value.stride(1) != D:
+        raise ValueError("decode store: key/value heads must be contiguous")
+    if slot_mapping.numel() != B:
+        raise ValueError("decode store: slot_mapping must hold one slot per sequence")
+    slots = _as_i32(slot_mapping.reshape(-1), "slot_mapping")
+    _lib.check(lib.vox_decode_attn_store(q.data_ptr(), q.stride(0), key.data_ptr(), value.data_ptr(), key.stride(0),
+                                         value.stride(0), slots.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                         num_blocks, block_size, bt.data_ptr(), bt.stride(0), max_blocks,
+                                         lens.data_ptr(), B, H, HK, D, float(softmax_scale), ws.data_ptr(),
+                                         ws.numel(), out.data_ptr(), _lib.stream_handle(dev)),
+               "decode_attn_store")
     return out
 
 
