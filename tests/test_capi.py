@@ -72,6 +72,25 @@ def test_decode_rejects_unsupported_shapes():
         assert msg in _err(), (over, _err())
 
 
+def _decode_store(**over):
+    p = ctypes.c_void_p(256)
+    a = dict(q=p, qs=16 * 128, key=p, value=p, ks=20 * 128, vs=20 * 128, slots=p, kc=p, vc=p, nb=4, bs=256, bt=p, bts=8,
+             mb=8, lens=p, b=2, h=16, hk=2, d=128, scale=0.088, ws=p, wsb=1 << 30, out=p, stream=None)
+    a.update(over)
+    return _lib.load().vox_decode_attn_store(*a.values())
+
+
+def test_decode_store_rejects_bad_arguments():
+    """The decode call with the store folded in: the store's own checks (rows 16-byte aligned, strides in whole
+    16-byte pieces and at least one row) before the decode's, and an empty batch is a no-op."""
+    assert _decode_store(b=0) == _lib.VOX_OK
+    for over, msg in [(dict(key=None), "null"), (dict(slots=None), "null"), (dict(ks=100), "key / value"),
+                      (dict(vs=128), "key / value"), (dict(value=ctypes.c_void_p(264)), "key / value"),
+                      (dict(d=64), "head_dim"), (dict(wsb=10), "workspace"), (dict(lens=None), "null")]:
+        assert _decode_store(**over) == _lib.VOX_EINVAL, over
+        assert msg in _err(), (over, _err())
+
+
 def test_decode_workspace_and_grid_choice():
     lib = _lib.load()
     assert lib.vox_decode_workspace_bytes(0) == 0
