@@ -161,6 +161,11 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   const int jq = lane >> 4;
   const int H = p.num_heads;
   const int max_ctx = p.max_blocks * p.block_size;
+  const int h = r16;
+  // per-lane byte offsets of the tile loads: K row r16, dims jq*8 + [0, 8) (+ 32 per k-step); V piece 0 = row
+  // lane / PPR, dims (lane % PPR) * 8 + [0, 8)
+  const uint32_t koff = (uint32_t)(r16 * TT::ROW + jq * 8) * 2u;
+  const uint32_t voff = (uint32_t)((lane / TT::PPR) * TT::ROW + (lane % TT::PPR) * 8) * 2u;
 
   // ---- block table into LDS and the step layout (a block-wide prefix sum over ceil(context / 16)). The lengths of
   // the first kThreads sequences and every table entry a thread stages are loaded before any of them is waited for:
@@ -243,48 +248,53 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
     if (tid == 0) p.steps[p.batch + 1] = G;
   }
 
-  // this workgroup's range [r, r1) and the sequence holding its first step: the last b with s_start[b] <= r
-  // (an empty sequence shares its start with the next one, so the last such b is not empty)
+  // this workgroup's range [r, r1)
   if (g >= G) return;  // workgroup-uniform; WG 0 (always active) published the layout
   const int r1 = (int)muldiv(g + 1, S, 0, G);
-  int r = (int)muldiv(g, S, 0, G);
-  int b = 0;
-  if (r < r1) {
-    int lo = 0, hi = p.batch;  // s_start[lo] <= r < s_start[hi]
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (uniform(s_start[mid]) <= r) lo = mid; else hi = mid;
-    }
-    b = lo;
-  }
+  const int r = (int)muldiv(g, S, 0, G);
 
-  const int h = r16;
+  // Sequence lookups are lane-parallel (a ballot over LDS values the lanes read together) rather than walks of
+  // dependent LDS reads: at config 4 a binary search for the range's first sequence and serial walks to each wave's
+  // first tile took 2.8 us between the layout and the first tile loads, with HBM idle (a call: 41.6 -> 40.7 us).
+  // The sequence holding range position x < S: the last b with s_start[b] <= x (an empty sequence shares its start
+  // with the next one, so the last such b is not empty); a search over chunks of 64 sequences, then inside the chunk.
+  auto seq_at = [&](int x) -> int {
+    const int nch = (p.batch + kWave - 1) / kWave;  // <= 8 at kMaxSeqPerLaunch
+    const int c0 = lane < nch ? s_start[lane * kWave] : INT32_MAX;
+    const uint64_t m0 = __builtin_amdgcn_ballot_w64(c0 <= x);  // chunk 0 at least (s_start[0] = 0)
+    const int ch = 63 - __builtin_clzll(m0);
+    const int i = ch * kWave + lane;
+    const int c1 = i <= p.batch ? s_start[i] : INT32_MAX;  // s_start[batch] = S > x
+    const uint64_t m1 = __builtin_amdgcn_ballot_w64(c1 <= x);
+    return ch * kWave + 63 - __builtin_clzll(m1);
+  };
+  // A round's window: lane k holds sequence wb + k (its steps [w_st, w_en), context, row, new-token slot), read in
+  // one LDS round trip; per-sequence values then come from the lane registers (v_readlane with a uniform index).
+  int w_st = 0, w_en = 0, w_ctx = 0, w_row = 0, w_snew = -1;
+  auto lane_val = [&](int v, int k) { return __builtin_amdgcn_readlane(v, k); };
+
   const int hg = h < H ? h / p.group : -1;
   uint16_t* vt = s_vt + w * kTile * VROW;
   // this lane's transposed-read address inside a d-tile: row jq*4 + r16/4, column 4*(r16%4)
   const uint16_t* vtr = vt + (jq * 4 + (r16 >> 2)) * VROW + 4 * (r16 & 3);
   constexpr int kMOff = kMaxHeads * kD;  // inside a slot: O [16 heads][128], then m[16], l[16] (log2 domain)
   constexpr int kLOff = kMOff + kMaxHeads;
-  // per-lane byte offsets of the tile loads: K row r16, dims jq*8 + [0, 8) (+ 32 per k-step); V piece 0 = row
-  // lane / PPR, dims (lane % PPR) * 8 + [0, 8)
-  const uint32_t koff = (uint32_t)(r16 * TT::ROW + jq * 8) * 2u;
-  const uint32_t voff = (uint32_t)((lane / TT::PPR) * TT::ROW + (lane % TT::PPR) * 8) * 2u;
   const float c = p.scale_log2;
 
-  auto start_of = [&](int bs) { return uniform(s_start[bs]); };
-  auto next_nonempty = [&](int bs) {  // bs or the first sequence after it that holds a tile
-    while (start_of(bs + 1) == start_of(bs)) ++bs;
-    return bs;
-  };
-  // block id of range tile t of sequence bs
-  auto block_of = [&](int bs, int t) -> int64_t {
-    const int col = (t - start_of(bs)) * kTile / p.block_size;
+  int wb = 0;       // the round window's first sequence
+  uint64_t segs = 0;  // the round's segments: window lanes of the non-empty sequences it covers
+  // block id of range tile t of the sequence at window lane k
+  auto block_of = [&](int k, int t) -> int64_t {
+    const int col = (t - lane_val(w_st, k)) * kTile / p.block_size;
+    const int bs = wb + k;
     if constexpr (BTL) return uniform(s_bt[bs * mb + col]);
     else return p.block_tables[(int64_t)bs * p.bt_stride + col];
   };
-  auto issue = [&](Tile<HK>& T, int64_t blk, int bs, int t) {  // loads of range tile t (sequence bs), block blk
+  // the round's next segment after window lane k
+  auto next_seg = [&](int k) { return __builtin_ctzll(k >= 63 ? 0ull : (segs >> (k + 1)) << (k + 1)); };
+  auto issue = [&](Tile<HK>& T, int64_t blk, int k, int t) {  // loads of range tile t (window lane k), block blk
     T.ok = blk >= 0 && blk < p.num_blocks;
-    const int tok = (t - start_of(bs)) * kTile;
+    const int tok = (t - lane_val(w_st, k)) * kTile;
     const int64_t slot0 = (T.ok ? blk : 0) * p.block_size + (tok % p.block_size);
     if (!p.slot_mapping) {
       load_tile<HK>(T, p, slot0, koff, voff);
@@ -292,45 +302,55 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
     }
     // store mode: the tile holds the new token when its slot lies in [slot0, slot0 + 16) (unmapped tiles are masked
     // whatever they read)
-    const int64_t dn = (int64_t)uniform(s_snew[bs]) - slot0;
+    const int bs = wb + k;
+    const int64_t dn = (int64_t)lane_val(w_snew, k) - slot0;
     const int r_new = dn >= 0 && dn < kTile ? (int)dn : -1;
     load_tile_new<HK>(T, p, slot0, koff, voff, r_new, p.new_k + (int64_t)bs * p.new_k_stride,
                       p.new_v + (int64_t)bs * p.new_v_stride);
   };
-  auto load_q = [&](u32x4 (&qv)[4], int bs) {  // query row of head r16: d = kq*32 + jq*8 + [0, 8)
-    const uint16_t* qb = p.q + (int64_t)uniform(s_row[bs]) * p.q_row_stride + (int64_t)(h < H ? h : 0) * kD + jq * 8;
+  auto load_q = [&](u32x4 (&qv)[4], int k) {  // query row of head r16: d = kq*32 + jq*8 + [0, 8)
+    const uint16_t* qb =
+        p.q + (int64_t)lane_val(w_row, k) * p.q_row_stride + (int64_t)(h < H ? h : 0) * kD + jq * 8;
 #pragma unroll
     for (int kq = 0; kq < 4; ++kq) qv[kq] = ld_g16(qb + kq * 32);
   };
 
   int rr = r;   // round start (range position)
-  int bb = b;   // its sequence
   while (rr < r1) {
-    // the round: up to kRoundSegs segments from rr
-    int re = rr, nseg = 0;
-    for (int bs = bb; nseg < kRoundSegs && re < r1; ++bs, ++nseg) {
-      bs = next_nonempty(bs);
-      re = min(r1, start_of(bs + 1));
+    // the round: up to kRoundSegs non-empty sequences from the one holding rr, those starting before r1, within
+    // one 64-sequence window (a round over a window with fewer segments ends at the window's last one)
+    wb = seq_at(rr);
+    {
+      const int sq = wb + lane;
+      const bool in = sq < p.batch;
+      w_st = in ? s_start[sq] : S;
+      w_en = in ? s_start[sq + 1] : S;
+      w_ctx = in ? s_ctx[sq] : 0;
+      w_row = in ? s_row[sq] : 0;
+      w_snew = in && p.slot_mapping ? s_snew[sq] : -1;
     }
+    const uint64_t cand = __builtin_amdgcn_ballot_w64(w_en > w_st && w_st < r1);  // lane 0 at least
+    const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(cand >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)cand, 0));
+    segs = __builtin_amdgcn_ballot_w64(((cand >> lane) & 1ull) && below < kRoundSegs);
+    const int nseg = __builtin_popcountll(segs);
+    const int re = min(r1, lane_val(w_en, 63 - __builtin_clzll(segs)));
     const int R = re - rr;
     auto share_lo = [&](int ww) { return rr + (int)(((int64_t)R * ww) / kWaves); };
     const int t_lo = share_lo(w), t_hi = share_lo(w + 1);
 
     if (t_lo < t_hi) {
-      // this wave's first tile: sequence bc (round segment kc)
-      int bc = next_nonempty(bb), kc = 0;
-      while (start_of(bc + 1) <= t_lo) {
-        bc = next_nonempty(bc + 1);
-        ++kc;
-      }
+      // this wave's first tile: window lane kcur, round segment kc
+      const uint64_t hold = __builtin_amdgcn_ballot_w64(((segs >> lane) & 1ull) && w_st <= t_lo && t_lo < w_en);
+      int kcur = __builtin_ctzll(hold);
+      int kc = __builtin_popcountll(segs & ((1ull << kcur) - 1ull));
       Tile<HK> T;
       u32x4 qv[4];
-      load_q(qv, bc);
-      issue(T, block_of(bc, t_lo), bc, t_lo);
-      // the tile to issue next (t_lo + 1: sequence bi) and its block id, read one tile ahead
-      int bi = bc;
-      if (t_lo + 1 < t_hi && t_lo + 1 >= start_of(bc + 1)) bi = next_nonempty(bc + 1);
-      int64_t blk_pf = t_lo + 1 < t_hi ? block_of(bi, t_lo + 1) : 0;
+      load_q(qv, kcur);
+      issue(T, block_of(kcur, t_lo), kcur, t_lo);
+      // the tile to issue next (t_lo + 1: window lane ki) and its block id, read one tile ahead
+      int ki = kcur;
+      if (t_lo + 1 < t_hi && t_lo + 1 >= lane_val(w_en, kcur)) ki = next_seg(kcur);
+      int64_t blk_pf = t_lo + 1 < t_hi ? block_of(ki, t_lo + 1) : 0;
 
       float m = -INFINITY;
       float lsum = 0.f;
@@ -416,18 +436,17 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
           for (int kk = 0; kk < TT::KC; ++kk) qop[kk] = hg == kk / 4 ? qv[kk % 4] : zero4();
           fresh = false;
         }
-        const int sbc = start_of(bc);
-        compute(T, (t - sbc) * kTile, uniform(s_ctx[bc]));
+        compute(T, (t - lane_val(w_st, kcur)) * kTile, lane_val(w_ctx, kcur));
         // the next tile's loads go out now, with the query first when it starts a new sequence; then the block id
         // of the tile after it
         if (t + 1 < t_hi) {
-          if (bi != bc) load_q(qv, bi);
-          issue(T, blk_pf, bi, t + 1);
-          int bn = bi;
-          if (t + 2 < t_hi && t + 2 >= start_of(bi + 1)) bn = next_nonempty(bi + 1);
-          blk_pf = t + 2 < t_hi ? block_of(bn, t + 2) : 0;
-          const bool seq_done = bi != bc;
-          if (seq_done) {  // sequence bc's share of this wave is done: its partial goes to slot w + kc
+          if (ki != kcur) load_q(qv, ki);
+          issue(T, blk_pf, ki, t + 1);
+          int kn = ki;
+          if (t + 2 < t_hi && t + 2 >= lane_val(w_en, ki)) kn = next_seg(ki);
+          blk_pf = t + 2 < t_hi ? block_of(kn, t + 2) : 0;
+          const bool seq_done = ki != kcur;
+          if (seq_done) {  // this wave's share of the current sequence is done: its partial goes to slot w + kc
             lsum = col_sum4(lsum);
             float* sl = s_slot + (w + kc) * kPartialFloats;
 #pragma unroll
@@ -441,10 +460,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
             fresh = true;
-            bc = bi;
+            kcur = ki;
             ++kc;
           }
-          bi = bn;
+          ki = kn;
         }
       }
       lsum = col_sum4(lsum);  // the last sequence of the share
@@ -463,10 +482,12 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
     constexpr int kTpr = kD / kDpt;                    // threads per head
     const int hh = tid / kTpr;
     const int d0 = (tid % kTpr) * kDpt;
-    int bs = bb;
-    for (int k = 0; k < nseg; ++k, ++bs) {
-      bs = next_nonempty(bs);
-      const int sb = start_of(bs), eb = start_of(bs + 1);
+    uint64_t rest = segs;
+    for (int k = 0; k < nseg; ++k) {
+      const int kl = __builtin_ctzll(rest);  // segment k's window lane
+      rest &= rest - 1ull;
+      const int bs = wb + kl;
+      const int sb = lane_val(w_st, kl), eb = lane_val(w_en, kl);
       const int a = max(rr, sb), e = min(re, eb);
       // the waves whose shares hold tiles of this segment, read in one pass (all loads before any use)
       float mw[kWaves], lw[kWaves];
@@ -502,7 +523,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
       if (a == sb && e == eb) {  // the whole sequence is in this workgroup's range: the output itself
         if (hh < H) {
           const float inv = L > 0.f ? 1.f / L : 0.f;
-          const int64_t row = uniform(s_row[bs]);
+          const int64_t row = lane_val(w_row, kl);
 #pragma unroll
           for (int i = 0; i < kDpt / 4; ++i)
             *reinterpret_cast<u32x2*>(p.out + row * p.out_row_stride + (int64_t)hh * kD + d0 + 4 * i) =
@@ -520,7 +541,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
     }
     __syncthreads();  // the slots and V tiles are free for the next round
     rr = re;
-    bb = bs;
   }
 }
 
