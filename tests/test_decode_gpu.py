@@ -101,6 +101,26 @@ def test_decode_split_grids_agree(grid):
         lib.vox_set_decode_workgroups(0)
 
 
+@pytest.mark.parametrize("grid", [1, 3, 256])
+def test_decode_sparse_batch_of_mostly_empty_rows(grid):
+    """300 rows, most of them empty (padded): the split kernel's rounds look sequences up in windows of 64 rows, so
+    a round can end at a window's last non-empty row before the workgroup's range does (runs of 60+ empty rows),
+    and elsewhere at eight non-empty rows (the dense run 200-210)."""
+    gen = torch.Generator().manual_seed(41)
+    lens = [0] * 300
+    for i in (5, 70, 71, 72, 140, 141, 299) + tuple(range(200, 211)):
+        lens[i] = int(torch.randint(1, 1500, (1,), generator=gen))
+    kc, vc, tables = paged_pool(gen, [max(n, 1) for n in lens], 400)
+    lib = _lib.load()
+    lib.vox_set_decode_workgroups(grid)
+    try:
+        (_, _), out = _check(randn(gen, len(lens), H, D), kc, vc, lens, tables, f"sparse, grid {grid}")
+    finally:
+        lib.vox_set_decode_workgroups(0)
+    empty = torch.tensor([n == 0 for n in lens], device=out.device)
+    assert int(out[empty].abs().sum()) == 0
+
+
 @pytest.mark.parametrize("lens", [[16384], [4096] * 4, [300] * 16 + [8192], [5, 9000, 3, 0, 2100, 64]],
                          ids=["1x16384", "4x4096", "16x300+8192", "mixed"])
 def test_decode_few_long_sequences(lens):
