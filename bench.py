@@ -410,7 +410,34 @@ def bench_prefill(dev):
     tf8 = flops / (ms8 * 1e-3) / 1e12
     out["config2_int8_output"] = dict(launch_us=round(ms8 * 1e3, 2), tflops=round(tf8, 2),
                                       pct_mfma_peak=round(100 * tf8 / MFMA_BF16_PEAK_TFLOPS, 2))
-    del qkv
+    # the same step in paged mode (the configuration's other mode): keys and values read through the block tables
+    # from 256-token blocks of a 512-block pool (each set its own pool and shuffled tables; 3 sets, 403 MB)
+    POOL, PSETS = 512, 3
+    kvp = _rand_bf16((PSETS, 2, POOL, BS, HK, D), 53, dev)
+    ptables = []
+    pgen = torch.Generator().manual_seed(54)
+    width = max((n + BS - 1) // BS for n in lens)
+    for _ in range(PSETS):
+        perm, at = torch.randperm(POOL, generator=pgen).tolist(), 0
+        t = torch.full((len(lens), width), -1, dtype=torch.int32)
+        for b, n in enumerate(lens):
+            nb = (n + BS - 1) // BS
+            t[b, :nb] = torch.tensor(perm[at:at + nb], dtype=torch.int32)
+            at += nb
+        ptables.append(t.to(dev))
+
+    def run_c2_paged():
+        for s in range(PSETS):
+            q = qkv[s][:, :H * D].view(T, H, D)
+            varlen_attention(q, None, None, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=max(lens),
+                             softmax_scale=SCALE, causal=True, block_table=ptables[s], k_cache=kvp[s, 0],
+                             v_cache=kvp[s, 1], out=o)
+
+    msp = _graph_ms(run_c2_paged, 20) / PSETS
+    tfp = flops / (msp * 1e-3) / 1e12
+    out["config2_paged"] = dict(launch_us=round(msp * 1e3, 2), tflops=round(tfp, 2),
+                                pct_mfma_peak=round(100 * tfp / MFMA_BF16_PEAK_TFLOPS, 2), input_sets=PSETS)
+    del qkv, kvp
     # supplementary compute-bound shape: 16 sequences x 2048 tokens, causal
     L, NB = 2048, 16
     T2 = L * NB

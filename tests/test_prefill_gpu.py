@@ -342,6 +342,22 @@ def test_uniform_lengths_over_several_key_tiles(causal):
     attn_close(out, want, f"uniform lengths, causal={causal}")
 
 
+def test_paged_table_wider_than_64_columns():
+    """Block ids of the first 64 table columns come from the row held across the wave's lanes; a longer row (here
+    64-token blocks under a 4930-key prefix: 78 columns) reads the columns past 63 from memory. Queries at the end
+    of the long sequence walk tiles on both sides of column 64."""
+    gen = torch.Generator().manual_seed(57)
+    nq = [30, 5]
+    nk = [4930, 70]
+    kc, vc, tables = paged_pool(gen, nk, sum((n + 63) // 64 for n in nk) + 3, block_size=64)
+    assert tables.shape[1] > 64
+    q = randn(gen, sum(nq), H, D)
+    out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), _cu(nq).to(DEV), _cu(nk).to(DEV), max(nq),
+                                 max(nk), softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
+    want = ref.varlen(q.float(), _cu(nq), _cu(nk), k_cache=kc, v_cache=vc, block_tables=tables)
+    attn_close(out, want, "paged table of 78 columns")
+
+
 @pytest.mark.parametrize("bs", [None, 256, 48])
 def test_grid_above_the_eight_wave_limit(bs):
     """A grid of more than 2048 workgroups (128 q tiles x 12 sequences x 2 kv heads), which the launcher runs with

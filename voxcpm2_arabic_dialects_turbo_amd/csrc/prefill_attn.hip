@@ -12,14 +12,15 @@
 // workgroups of 4 waves of 16. GQA shares every K/V tile across the group's heads.
 // Per 64-key tile K and V go from global memory straight into LDS (range-checked buffer loads with the lds bit: no
 // register staging; rows past the keys and unmapped blocks read as zeros), double-buffered, with the 16-byte chunks
-// of each 256-byte row permuted so that the fragment reads meet no bank conflicts; each wave computes S^T[64 keys x its rows] = K Q^T with Q^T held in
-// registers, an online softmax in fp32 (exp2, log2-prescaled scale), and O^T[128 d x rows] += V^T P^T, where P^T
-// comes out of the score MFMA already in B-operand layout and V^T is read with ds_read_b64_tr_b16 (two transposed
-// reads give a lane the 8 keys of one d column). The next tile's loads are issued before the current tile is
-// computed and waited for only at the tile's one barrier; in paged mode the block ids are read one tile further
-// ahead. The causal / length mask is only evaluated on tiles that reach past the first query's position or past
-// the keys. Large grids deal contiguous work ranges per XCD, so the query tiles that re-read a sequence's K/V find
-// it in that XCD's L2. (Paged caches whose block size is not a multiple of 64 stage per-piece loads through
+// of each 256-byte row permuted so that the fragment reads meet no bank conflicts; each wave computes
+// S^T[64 keys x its rows] = K Q^T with Q^T held in registers, an online softmax in fp32 (exp2, log2-prescaled scale),
+// and O^T[128 d x rows] += V^T P^T, where P^T comes out of the score MFMA already in B-operand layout and V^T is read
+// with ds_read_b64_tr_b16 (two transposed reads give a lane the 8 keys of one d column). The next tile's loads are
+// issued before the current tile is computed and waited for only at the tile's one barrier; in paged mode the
+// sequence's block-table row is held across the wave's lanes (one column per lane) and each tile's block id taken
+// with v_readlane. The causal / length mask is only evaluated on tiles that reach past the first query's position or
+// past the keys. Large grids deal contiguous work ranges per XCD, so the query tiles that re-read a sequence's K/V
+// find it in that XCD's L2. (Paged caches whose block size is not a multiple of 64 stage per-piece loads through
 // registers instead.)
 //
 // int8 output (QUANT; reference: the QUANT epilogues of kernels/prefill_attn.py:84-92 and kernels/short_attn.py:
@@ -82,9 +83,13 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
   const int g = QUANT ? half : gz;
   auto& ks = ks_all[half];
   auto& vs2 = vs_all[half];
-  // the sequence bounds, and the first key tile's block id (table column 0) beside them rather than after them
+  // the sequence bounds, and (paged tiles) the sequence's block-table row beside them rather than after them: lane c
+  // holds column c (c < 64), so the loop takes each tile's block id with v_readlane instead of a load. (A load per
+  // tile, one tile ahead, made the compiler wait for it, and with it for the next tile's DMA, right after issuing
+  // both: every step waited a full DMA round trip before its scores.)
   int q0, nq, k0, nk;
-  int bid0 = 0;
+  int bid0 = 0;     // column 0, for the first tile's DMA (a scalar load: the DMA need not wait for the row's lanes)
+  int bt_row = -1;
   {
     int q1, k1;
     q0 = b * p.uniform_q;
@@ -99,7 +104,11 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
       k0 = p.cu_k[b];
       k1 = p.cu_k[b + 1];
     }
-    if constexpr (KV == kPagedTiles) bid0 = p.block_tables[(int64_t)b * p.bt_stride];
+    if constexpr (KV == kPagedTiles) {
+      bid0 = p.block_tables[(int64_t)b * p.bt_stride];
+      const int col = (int)(threadIdx.x & 63);
+      if (col < p.max_blocks) bt_row = p.block_tables[(int64_t)b * p.bt_stride + col];
+    }
     nq = q1 - q0;
     nk = k1 - k0;
   }
@@ -170,7 +179,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
   auto fetch_bids = [&](int kv0) {
     if constexpr (!paged) return;
     if constexpr (blk_tiles) {
-      tile_bid = p.block_tables[(int64_t)b * p.bt_stride + min(kv0, nk - 1) / p.block_size];
+      const int col = min(kv0, nk - 1) / p.block_size;  // wave-uniform
+      tile_bid = col < 64 ? __builtin_amdgcn_readlane(bt_row, col)
+                          : p.block_tables[(int64_t)b * p.bt_stride + col];  // tables wider than 64 columns
       return;
     }
 #pragma unroll
@@ -514,8 +525,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
     if (kv_end > 0) {
       tile_bid = bid0;
       dma(kt0[half], vt0[half], 0);
+      wait_vmem_all();  // the query, tile 0 and the table row
       fetch_bids(kBK);
-      wait_vmem_all();  // the query and tile 0
       __syncthreads();
       for (int kv0 = 0; kv0 < kv_end; kv0 += 2 * kBK) {
         step(kv0, kt0[half], vt0[half], kt1[half], vt1[half]);
