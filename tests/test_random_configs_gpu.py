@@ -1,0 +1,82 @@
+"""Seeded random configurations of the decode and varlen prefill kernels against the oracle (max-abs 2e-2,
+mean-abs 2e-3): batch sizes, ragged and empty lengths, cached prefixes, block sizes, head groupings, split grids,
+causal and non-causal, packed and paged keys drawn together, so that combinations the targeted tests do not name are
+exercised too. Each case is small enough for the oracle's per-sequence loop."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as ref
+from tests._util import D, attn_close, paged_pool, randn
+from voxcpm2_arabic_dialects_turbo_amd import _lib
+from voxcpm2_arabic_dialects_turbo_amd.ops import decode_attention, flash_attn_varlen_func
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+SCALE = D ** -0.5
+
+
+def _cu(lens):
+    return torch.tensor([0] + np.cumsum(lens).tolist(), dtype=torch.int32)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_decode_configurations(seed):
+    gen = torch.Generator().manual_seed(1000 + seed)
+    pick = lambda xs: xs[int(torch.randint(len(xs), (1,), generator=gen))]
+    h, hk = pick([(16, 2), (8, 1), (16, 1), (4, 2)])
+    bs = pick([32, 64, 256])  # the decode ABI takes block sizes that are multiples of 32
+    B = int(torch.randint(1, 300, (1,), generator=gen))
+    lens = []
+    for _ in range(B):
+        u = float(torch.rand(1, generator=gen))
+        lens.append(0 if u < 0.15 else int(torch.randint(1, 200 if u < 0.5 else 3000, (1,), generator=gen)))
+    pool = sum((max(n, 1) + bs - 1) // bs for n in lens) + 2
+    kc, vc, tables = paged_pool(gen, [max(n, 1) for n in lens], pool, block_size=bs, hk=hk)
+    q = randn(gen, B, h, D)
+    grid = pick([0, 0, 5, 100])
+    lib = _lib.load()
+    lib.vox_set_decode_workgroups(grid)
+    try:
+        out = decode_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), torch.tensor(lens, dtype=torch.int32, device=DEV),
+                               tables.to(DEV), SCALE)
+        torch.cuda.synchronize()
+    finally:
+        lib.vox_set_decode_workgroups(0)
+    want = ref.decode(q.float(), kc, vc, lens, tables, SCALE)
+    attn_close(out, want, f"seed {seed}: B={B} heads {h}/{hk} block {bs} grid {grid}")
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_varlen_prefill_configurations(seed):
+    gen = torch.Generator().manual_seed(2000 + seed)
+    pick = lambda xs: xs[int(torch.randint(len(xs), (1,), generator=gen))]
+    h, hk = pick([(16, 2), (8, 1), (16, 4), (16, 16)])
+    paged = bool(torch.randint(2, (1,), generator=gen))
+    causal = bool(torch.randint(4, (1,), generator=gen))  # causal three times in four
+    B = int(torch.randint(1, 12, (1,), generator=gen))
+    nq = [int(torch.randint(1, 300, (1,), generator=gen)) for _ in range(B)]
+    if paged:
+        bs = pick([32, 64, 256])
+        nk = [n + (int(torch.randint(0, 600, (1,), generator=gen)) if causal else 0) for n in nq]
+        pool = sum((n + bs - 1) // bs for n in nk) + 2
+        kc, vc, tables = paged_pool(gen, nk, pool, block_size=bs, hk=hk)
+    else:
+        nk = list(nq)
+        k, v = randn(gen, sum(nk), hk, D), randn(gen, sum(nk), hk, D)
+    q = randn(gen, sum(nq), h, D)
+    cq, ck = _cu(nq), _cu(nk)
+    if paged:
+        out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), cq.to(DEV), ck.to(DEV), max(nq), max(nk),
+                                     softmax_scale=SCALE, causal=causal, block_table=tables.to(DEV))
+        want = ref.varlen(q.float(), cq, ck, scale=SCALE, causal=causal, k_cache=kc, v_cache=vc,
+                          block_tables=tables)
+    else:
+        out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), cq.to(DEV), ck.to(DEV), max(nq), max(nk),
+                                     softmax_scale=SCALE, causal=causal)
+        want = ref.varlen(q.float(), cq, ck, scale=SCALE, causal=causal, k=k, v=v)
+    torch.cuda.synchronize()
+    attn_close(out, want, f"seed {seed}: B={B} heads {h}/{hk} paged={paged} causal={causal}")
