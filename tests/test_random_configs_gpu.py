@@ -80,3 +80,41 @@ def test_random_varlen_prefill_configurations(seed):
         want = ref.varlen(q.float(), cq, ck, scale=SCALE, causal=causal, k=k, v=v)
     torch.cuda.synchronize()
     attn_close(out, want, f"seed {seed}: B={B} heads {h}/{hk} paged={paged} causal={causal}")
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_int8_prefill_configurations(seed):
+    """The int8-output prefill (fused epilogue or, for long causal batches, the bf16 pass and the quantization
+    pass) under the int8 tests' bounds, with or without inv_smooth."""
+    from tests.test_prefill_int8_gpu import _check
+    from voxcpm2_arabic_dialects_turbo_amd.ops import varlen_attention
+
+    gen = torch.Generator().manual_seed(3000 + seed)
+    pick = lambda xs: xs[int(torch.randint(len(xs), (1,), generator=gen))]
+    h, hk = pick([(16, 2), (8, 1), (16, 1)])
+    paged = bool(torch.randint(2, (1,), generator=gen))
+    causal = bool(torch.randint(4, (1,), generator=gen))
+    B = int(torch.randint(1, 11, (1,), generator=gen))
+    nq = [int(torch.randint(1, 320, (1,), generator=gen)) for _ in range(B)]
+    inv = torch.rand(h * D, generator=gen) + 0.5 if bool(torch.randint(2, (1,), generator=gen)) else None
+    q = randn(gen, sum(nq), h, D)
+    cq = _cu(nq)
+    if paged:
+        bs = pick([64, 256])
+        nk = [n + (int(torch.randint(0, 400, (1,), generator=gen)) if causal else 0) for n in nq]
+        kc, vc, tables = paged_pool(gen, nk, sum((n + bs - 1) // bs for n in nk) + 2, block_size=bs, hk=hk)
+        ck = _cu(nk)
+        out = varlen_attention(q.to(DEV), None, None, cu_seqlens_q=cq.to(DEV), cu_seqlens_k=ck.to(DEV),
+                               max_seqlen_q=max(nq), softmax_scale=SCALE, causal=causal, block_table=tables.to(DEV),
+                               k_cache=kc.to(DEV), v_cache=vc.to(DEV), quant=True,
+                               inv_smooth=None if inv is None else inv.to(DEV))
+        want = ref.varlen(q.float(), cq, ck, scale=SCALE, causal=causal, k_cache=kc, v_cache=vc,
+                          block_tables=tables)
+    else:
+        k, v = randn(gen, sum(nq), hk, D), randn(gen, sum(nq), hk, D)
+        out = varlen_attention(q.to(DEV), k.to(DEV), v.to(DEV), cu_seqlens_q=cq.to(DEV), cu_seqlens_k=cq.to(DEV),
+                               max_seqlen_q=max(nq), softmax_scale=SCALE, causal=causal, quant=True,
+                               inv_smooth=None if inv is None else inv.to(DEV))
+        want = ref.varlen(q.float(), cq, cq, scale=SCALE, causal=causal, k=k, v=v)
+    torch.cuda.synchronize()
+    _check(out, want, f"seed {seed}: B={B} heads {h}/{hk} paged={paged} causal={causal}", inv)
