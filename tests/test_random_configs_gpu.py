@@ -118,3 +118,37 @@ def test_random_int8_prefill_configurations(seed):
         want = ref.varlen(q.float(), cq, cq, scale=SCALE, causal=causal, k=k, v=v)
     torch.cuda.synchronize()
     _check(out, want, f"seed {seed}: B={B} heads {h}/{hk} paged={paged} causal={causal}", inv)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_decode_with_the_store_configurations(seed):
+    """The decode call with the step's store folded in (what Attention.forward runs for a decode step) against the
+    oracle's store followed by its decode: outputs within the tolerance, caches bit-exact. The new token sits at each
+    sequence's last position; padded rows (context 0, slot -1) among them; random grids."""
+    gen = torch.Generator().manual_seed(4000 + seed)
+    pick = lambda xs: xs[int(torch.randint(len(xs), (1,), generator=gen))]
+    h, hk = pick([(16, 2), (8, 1)])
+    bs = pick([32, 256])
+    B = int(torch.randint(1, 200, (1,), generator=gen))
+    lens = [0 if float(torch.rand(1, generator=gen)) < 0.1 else int(torch.randint(1, 2500, (1,), generator=gen))
+            for _ in range(B)]
+    kc, vc, tables = paged_pool(gen, [max(n, 1) for n in lens], sum(-(-max(n, 1) // bs) for n in lens) + 2,
+                                block_size=bs, hk=hk)
+    q, key, value = randn(gen, B, h, D), randn(gen, B, hk, D), randn(gen, B, hk, D)
+    slots = torch.tensor([-1 if n == 0 else int(tables[b, (n - 1) // bs]) * bs + (n - 1) % bs
+                          for b, n in enumerate(lens)], dtype=torch.int32)
+    k_ref, v_ref = kc.clone(), vc.clone()
+    ref.store_kvcache(key, value, k_ref, v_ref, slots)
+    want = ref.decode(q.float(), k_ref, v_ref, lens, tables, SCALE)
+    grid = pick([0, 7, 300])
+    lib = _lib.load()
+    lib.vox_set_decode_workgroups(grid)
+    try:
+        k1, v1 = kc.to(DEV), vc.to(DEV)
+        out = decode_attention(q.to(DEV), k1, v1, torch.tensor(lens, dtype=torch.int32, device=DEV), tables.to(DEV),
+                               SCALE, key=key.to(DEV), value=value.to(DEV), slot_mapping=slots.to(DEV))
+        torch.cuda.synchronize()
+    finally:
+        lib.vox_set_decode_workgroups(0)
+    attn_close(out, want, f"seed {seed}: B={B} heads {h}/{hk} block {bs} grid {grid}")
+    assert torch.equal(k1.cpu(), k_ref) and torch.equal(v1.cpu(), v_ref), f"seed {seed}: caches differ"
