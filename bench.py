@@ -51,9 +51,11 @@ def parse_args():
 
 # ---------------------------------------------------------------------------------------------------------------------
 
-def _graph_ms(fn, reps: int, warm: int = 3) -> float:
+def _graph_ms(fn, reps: int, warm: int = 3, warm_s: float = 0.15) -> float:
     """Captures fn() in a HIP graph (after one eager warm-up call) and returns ms per replay over `reps` replays,
-    timed by HIP events on the current stream."""
+    timed by HIP events on the current stream. The untimed warm-up replays run for at least `warm_s` seconds (and
+    `warm` replays): the GPU's clocks take some 0.1 s of sustained load to settle, and a leg timed straight after a
+    lighter one reads up to 25 % slow (16 x 2048 prefill: 361 -> 279 us over its first ~0.1 s)."""
     import torch
 
     fn()
@@ -61,8 +63,11 @@ def _graph_ms(fn, reps: int, warm: int = 3) -> float:
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         fn()
-    for _ in range(warm):
+    t0, n = time.perf_counter(), 0
+    while n < warm or time.perf_counter() - t0 < warm_s:
         g.replay()
+        torch.cuda.synchronize()
+        n += 1
     torch.cuda.synchronize()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()

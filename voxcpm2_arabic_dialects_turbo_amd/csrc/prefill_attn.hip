@@ -282,16 +282,14 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
       alpha[rt] = up ? fast_exp2(m[rt] - tm) : 1.f;  // exp2(-inf) = 0 on a row's first update
       m[rt] = up ? tm : m[rt];
       const float mu = m[rt] == -INFINITY ? 0.f : m[rt];
-      float ps = 0.f;
+      float s4[4];  // the row sum as a tree (depth 4, not a chain of 16 dependent adds)
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const float e = fast_exp2(fmaf(sc[kt][rt][rr], c, -mu));
-          sc[kt][rt][rr] = e;
-          ps += e;
-        }
-      l[rt] = l[rt] * alpha[rt] + ps;
+        for (int rr = 0; rr < 4; ++rr) sc[kt][rt][rr] = fast_exp2(fmaf(sc[kt][rt][rr], c, -mu));
+        s4[kt] = (sc[kt][rt][0] + sc[kt][rt][1]) + (sc[kt][rt][2] + sc[kt][rt][3]);
+      }
+      l[rt] = l[rt] * alpha[rt] + ((s4[0] + s4[1]) + (s4[2] + s4[3]));
     }
     // P^T B operands; k-step k2 covers keys k2*32 + {jq*4 + [0,4), 16 + jq*4 + [0,4)} for lane jq, the order in
     // which the score MFMA left them in the lane's registers
@@ -316,7 +314,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       const float mu = m[rt] == -INFINITY ? 0.f : m[rt];
-      float sum = 0.f;
+      float s2[8];  // pair sums, added as a tree (depth 4, not a chain of 16 dependent adds)
       uint32_t pk[8];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
@@ -324,10 +322,10 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
         for (int h2 = 0; h2 < 2; ++h2) {
           const float e0 = fast_exp2(fmaf(sc[kt][rt][2 * h2], c, -mu));
           const float e1 = fast_exp2(fmaf(sc[kt][rt][2 * h2 + 1], c, -mu));
-          sum += e0;
-          sum += e1;
+          s2[kt * 2 + h2] = e0 + e1;
           pk[kt * 2 + h2] = pack_bf16x2(e0, e1);
         }
+      const float sum = ((s2[0] + s2[1]) + (s2[2] + s2[3])) + ((s2[4] + s2[5]) + (s2[6] + s2[7]));
       ps[rt] = sum;
       big = big || !(sum <= 0x1p62f);  // also catches inf
 #pragma unroll
@@ -433,16 +431,17 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
     const uint32_t krd0 = (uint32_t)(r16 * 256 + ((jq ^ r16) << 4));
     auto scores_d = [&](const uint8_t* kd, f32x4 (&sc)[4][RT]) {
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) sc[kt][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc) {
+      for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
           const u32x4 a = *reinterpret_cast<const u32x4*>(kd + kt * 4096 + (krd0 ^ (uint32_t)(kc << 6)));
 #pragma unroll
           for (int rt = 0; rt < RT; ++rt) sc[kt][rt] = mfma_16x16x32(a, qop[rt][kc], sc[kt][rt]);
         }
-      }
       __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
