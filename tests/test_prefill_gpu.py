@@ -267,6 +267,42 @@ def test_prefill_scores_growing_across_key_tiles():
     attn_close(out2, want, "growing scores, paged")
 
 
+@pytest.mark.parametrize("paged", [False, True])
+def test_scores_growing_across_key_tiles_in_the_32_row_form(paged):
+    """The same growing scores in a grid above 2048 workgroups (one 2100-token sequence beside seven short ones:
+    132 q tiles x 8 x 2), which takes the 4-wave x 32-row form and its pipelined loop, where a tile whose scores
+    pass the running max is redone at the start of the next step; about every second key tile of the long sequence
+    takes that path."""
+    gen = torch.Generator().manual_seed(59)
+    lens = [2100] + [int(x) for x in torch.randint(20, 120, (7,), generator=gen)]
+    T = sum(lens)
+    u = torch.randn(HK, D, generator=gen)
+    q = (u.repeat_interleave(H // HK, dim=0).expand(T, H, D) + 0.3 * torch.randn(T, H, D, generator=gen))
+    q = q.to(torch.bfloat16)
+    k = randn(gen, T, HK, D).float()
+    v = randn(gen, T, HK, D)
+    for j in range(64, lens[0]):
+        k[j] = u * (0.05 * (j - 63))
+    k = k.to(torch.bfloat16)
+    cu = _cu(lens)
+    want = ref.varlen(q.float(), cu, cu, k=k, v=v)
+    if paged:
+        kc, vc, tables = paged_pool(gen, lens, sum((n + BLOCK - 1) // BLOCK for n in lens) + 2)
+        at = 0
+        for b, n in enumerate(lens):
+            for j in range(n):
+                kc[tables[b, j // BLOCK], j % BLOCK] = k[at + j]
+                vc[tables[b, j // BLOCK], j % BLOCK] = v[at + j]
+            at += n
+        out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), cu.to(DEV), cu.to(DEV), max(lens),
+                                     max(lens), softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
+    else:
+        out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), cu.to(DEV), cu.to(DEV), max(lens), max(lens),
+                                     softmax_scale=SCALE, causal=True)
+    assert torch.isfinite(out.float()).all()
+    attn_close(out, want, f"growing scores, 32-row form, paged={paged}")
+
+
 def _without_columns(table, drop, width):
     """A block-table row without the given columns, -1 padded to ``width``."""
     kept = [int(x) for j, x in enumerate(table.tolist()) if j not in drop and x >= 0]
