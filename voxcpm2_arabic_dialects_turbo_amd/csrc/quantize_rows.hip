@@ -7,10 +7,10 @@
 // its fp32 accumulators (reference: the QUANT epilogue of nanovllm_voxcpm/kernels/prefill_attn.py:84-92, which the
 // reference's unfused path applies to flash-attn's bf16 output the same way).
 //
-// One wave per row: lane l takes the 16-byte chunks l, l + 64, ... of the row (8 values each, coalesced), the row max
-// is a wave reduction (DPP and lane swaps, no LDS), and each chunk leaves as 8 int8 codes in one 8-byte store. Short
-// and latency-bound (one load round trip, a reduction, the stores); the rows are the attention pass's output, which
-// runs just before it on the stream.
+// One wave per row: lane l takes the 16-byte chunks l, l + 64, ... of the row (8 values each, coalesced; all of a
+// lane's loads, and those of inv_smooth, issued before any is used), the row max is a wave reduction (DPP and lane
+// swaps, no LDS), and each chunk leaves as 8 int8 codes in one 8-byte store. Short and latency-bound (one load round
+// trip, a reduction, the stores); the rows are the attention pass's output, which runs just before it on the stream.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -23,6 +23,7 @@ namespace {
 constexpr int kQWaves = 4;
 constexpr int kQMaxChunks = 4;  // 16-byte chunks per lane: rows of up to 64 x 4 x 8 = 2048 values (16 heads)
 
+template <bool SMOOTH>
 __global__ __launch_bounds__(64 * kQWaves) void quantize_rows_kernel(const uint16_t* __restrict__ x, int64_t rows,
                                                                      int row_elems, const float* __restrict__ inv_smooth,
                                                                      int8_t* __restrict__ out_q, int64_t out_row_stride,
@@ -32,26 +33,34 @@ __global__ __launch_bounds__(64 * kQWaves) void quantize_rows_kernel(const uint1
   if (row >= rows) return;  // wave-uniform
   const int nchunk = row_elems >> 3;
   const uint16_t* xr = x + row * row_elems;
+  // every load first, unconditional and in bounds (a lane past the row rereads its last chunk, then ignores it), so
+  // they share one round trip (guarded loads had each waited for the one before)
+  u32x4 w[kQMaxChunks];
+  f32x4 sa[kQMaxChunks], sb[kQMaxChunks];
+#pragma unroll
+  for (int i = 0; i < kQMaxChunks; ++i) w[i] = ld_g16(xr + min(lane + 64 * i, nchunk - 1) * 8);
+#pragma unroll
+  for (int i = 0; i < kQMaxChunks; ++i) {
+    if constexpr (SMOOTH) {
+      const float* sp = inv_smooth + min(lane + 64 * i, nchunk - 1) * 8;
+      sa[i] = *reinterpret_cast<const f32x4*>(sp);
+      sb[i] = *reinterpret_cast<const f32x4*>(sp + 4);
+    } else {
+      sa[i] = sb[i] = f32x4{1.f, 1.f, 1.f, 1.f};
+    }
+  }
   float v[kQMaxChunks][8];
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < kQMaxChunks; ++i) {
-    const int c = lane + 64 * i;
-    if (c < nchunk) {
-      const u32x4 w = ld_g16(xr + c * 8);
-      f32x4 s0 = f32x4{1.f, 1.f, 1.f, 1.f}, s1 = s0;
-      if (inv_smooth) {
-        s0 = *reinterpret_cast<const f32x4*>(inv_smooth + c * 8);
-        s1 = *reinterpret_cast<const f32x4*>(inv_smooth + c * 8 + 4);
-      }
+    const bool live = lane + 64 * i < nchunk;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[i][2 * j] = bf16_bits_to_float(w[j] & 0xFFFFu) * (j < 2 ? s0[2 * j] : s1[2 * j - 4]);
-        v[i][2 * j + 1] = bf16_bits_to_float(w[j] >> 16) * (j < 2 ? s0[2 * j + 1] : s1[2 * j - 3]);
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[i][e]));
+    for (int j = 0; j < 4; ++j) {
+      v[i][2 * j] = bf16_bits_to_float(w[i][j] & 0xFFFFu) * (j < 2 ? sa[i][2 * j] : sb[i][2 * j - 4]);
+      v[i][2 * j + 1] = bf16_bits_to_float(w[i][j] >> 16) * (j < 2 ? sa[i][2 * j + 1] : sb[i][2 * j - 3]);
     }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = live ? fmaxf(amax, fabsf(v[i][e])) : amax;
   }
   amax = wave_max(amax);
   const float scale = fmaxf(amax, 1e-6f) / 127.f;
@@ -86,8 +95,12 @@ hipError_t launch_quantize_rows(const uint16_t* x, int64_t rows, int row_elems, 
   if (row_elems <= 0 || row_elems % 8 || row_elems > 64 * 8 * kQMaxChunks) return hipErrorInvalidValue;
   const int64_t grid = (rows + kQWaves - 1) / kQWaves;
   if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
-  quantize_rows_kernel<<<dim3((unsigned)grid), dim3(64 * kQWaves), 0, stream>>>(x, rows, row_elems, inv_smooth, out_q,
-                                                                              out_row_stride, out_scale);
+  if (inv_smooth)
+    quantize_rows_kernel<true><<<dim3((unsigned)grid), dim3(64 * kQWaves), 0, stream>>>(x, rows, row_elems, inv_smooth,
+                                                                                      out_q, out_row_stride, out_scale);
+  else
+    quantize_rows_kernel<false><<<dim3((unsigned)grid), dim3(64 * kQWaves), 0, stream>>>(x, rows, row_elems, nullptr,
+                                                                                       out_q, out_row_stride, out_scale);
   return hipGetLastError();
 }
 
