@@ -364,7 +364,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
       // scale goes into the exp2 argument (one FMA); the running max moves (rescaling acc and lsum) only when the
       // tile max exceeds it by more than 8 in log2 units (p <= 256, exact after the final 1 / l); the masks and zero
       // selects run only on a tile that is not fully valid.
-      auto compute = [&](const Tile<HK>& T, int t0, int tok_end) {
+      auto compute = [&](const Tile<HK>& T, int t0, int tok_end, auto&& between) {
         f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < TT::KC; ++kk) s = mfma_16x16x32(T.k[kk], qop[kk], s);
@@ -409,6 +409,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
           }
         }
         wave_lds_sync();
+        between();  // the tile's registers are free: the next tile's loads go out before P V
 
         // P^T operand: k-slots jq*4 + [0, 4) = tokens jq*4 + [0, 4)
         const uint32_t p01 = pack_bf16x2(x[0], x[1]);
@@ -436,12 +437,14 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
           for (int kk = 0; kk < TT::KC; ++kk) qop[kk] = hg == kk / 4 ? qv[kk % 4] : zero4();
           fresh = false;
         }
-        compute(T, (t - lane_val(w_st, kcur)) * kTile, lane_val(w_ctx, kcur));
-        // the next tile's loads go out now, with the query first when it starts a new sequence; then the block id
-        // of the tile after it
+        compute(T, (t - lane_val(w_st, kcur)) * kTile, lane_val(w_ctx, kcur), [&]() {
+          if (t + 1 < t_hi) {
+            if (ki != kcur) load_q(qv, ki);
+            issue(T, blk_pf, ki, t + 1);
+          }
+        });
+        // then the block id of the tile after it
         if (t + 1 < t_hi) {
-          if (ki != kcur) load_q(qv, ki);
-          issue(T, blk_pf, ki, t + 1);
           int kn = ki;
           if (t + 2 < t_hi && t + 2 >= lane_val(w_en, ki)) kn = next_seg(ki);
           blk_pf = t + 2 < t_hi ? block_of(kn, t + 2) : 0;
