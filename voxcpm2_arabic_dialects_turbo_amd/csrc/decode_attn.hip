@@ -374,24 +374,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4)
           x[q4] = full || (T.ok && (t0 + jq * 4 + q4) < tok_end) ? s[q4] : -INFINITY;
-        const float tm = col_max4(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]))) * c;
-        const bool up = tm > m + 8.f;
-        if (__builtin_amdgcn_ballot_w64(up) != 0) {  // wave-uniform
-          const float alpha = up ? fast_exp2(m - tm) : 1.f;  // exp2(-inf) = 0 on the first update
-          m = up ? tm : m;
-          lsum *= alpha;
-#pragma unroll
-          for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
-        }
-        const float mu = m == -INFINITY ? 0.f : m;
-        float ps = 0.f;
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          x[q4] = fast_exp2(fmaf(x[q4], c, -mu));
-          ps += x[q4];
-        }
-        lsum += ps;
-
         // V tile -> LDS, row-major, 16-byte stores; rows of tokens past tok_end or of an unmapped block are zeroed
         // (they meet p = 0 in P V, and unwritten cache slots may hold any bit pattern)
         if (full) {
@@ -409,7 +391,25 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
           }
         }
         wave_lds_sync();
-        between();  // the tile's registers are free: the next tile's loads go out before P V
+        between();  // the tile's registers are free: the next tile's loads go out before the softmax and P V
+
+        const float tm = col_max4(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]))) * c;
+        const bool up = tm > m + 8.f;
+        if (__builtin_amdgcn_ballot_w64(up) != 0) {  // wave-uniform
+          const float alpha = up ? fast_exp2(m - tm) : 1.f;  // exp2(-inf) = 0 on the first update
+          m = up ? tm : m;
+          lsum *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+        }
+        const float mu = m == -INFINITY ? 0.f : m;
+        float ps = 0.f;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          x[q4] = fast_exp2(fmaf(x[q4], c, -mu));
+          ps += x[q4];
+        }
+        lsum += ps;
 
         // P^T operand: k-slots jq*4 + [0, 4) = tokens jq*4 + [0, 4)
         const uint32_t p01 = pack_bf16x2(x[0], x[1]);
