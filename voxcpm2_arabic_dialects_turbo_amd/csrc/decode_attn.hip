@@ -547,38 +547,16 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   }
 }
 
-// Writes the sequences that decode_kernel left as partials, and the zeros of empty rows (in varlen mode only those of
-// one-query sequences; the others belong to the prefill kernel). One workgroup per sequence, thread = (head, 8 dims). Sequence b covers steps [sb, eb) of the layout decode_kernel published in
-// `steps`, with the number G of workgroups it used; workgroup g of G covers [floor(g S / G), floor((g + 1) S / G))
-// (at least one step, as G <= S), and the workgroups touching b, g_first..g_last below, each left a partial at slot
-// b + g. Online rescale over the partials (fp32), the loads of kMergeBatch partials in flight together. Runs after
-// decode_kernel on the same stream, which makes the partials visible.
-__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs p) {
-  const int b = blockIdx.x;
-  const int tid = threadIdx.x;
-  if (p.slot_mapping) {  // store mode: the new K / V row into the cache, now that every read of the split is done
-    const int row_elems = p.group ? p.num_heads / p.group * kD : 0;  // HK x 128
-    const int64_t slot = p.slot_mapping[b];
-    const int chunk = tid & 127;  // 16-byte chunk of the row: threads 0-127 K, 128-255 V
-    if (slot >= 0 && slot < p.num_blocks * p.block_size && chunk * 8 < row_elems) {
-      const bool is_v = tid >= 128;
-      const uint16_t* src = (is_v ? p.new_v + (int64_t)b * p.new_v_stride : p.new_k + (int64_t)b * p.new_k_stride);
-      uint16_t* dst = const_cast<uint16_t*>(is_v ? p.v_cache : p.k_cache) + slot * row_elems;
-      *reinterpret_cast<u32x4*>(dst + chunk * 8) = ld_g16(src + chunk * 8);
-    }
-  }
+// The merge of sequence b's split-KV partials into its output row (decode_merge_kernel).
+// steps: the layout's total S, sequence b's first and end steps sb, eb, and the active workgroups G (with S >= 1, none
+// has an empty range); [c0, c1): b's query rows (b's row alone outside varlen mode).
+__device__ __forceinline__ void merge_row(const DecodeArgs& p, int b, int tid, int64_t S, int64_t sb, int64_t eb,
+                                          int64_t G, int c0, int c1) {
   const int hh = tid >> 4;
   const int d0 = (tid & 15) * 8;
   const int H = p.num_heads;
-  const int64_t S = p.steps[p.batch];
-  const int64_t sb = p.steps[b];
-  const int64_t eb = p.steps[b + 1];
-  const int64_t G = p.steps[p.batch + 1];  // active workgroups (with S >= 1, none has an empty range)
-  int64_t row = b;
-  if (p.cu_q) {
-    row = p.cu_q[b];
-    if (p.cu_q[b + 1] - row != 1) return;  // not a one-query row: the prefill kernel writes it
-  }
+  const int64_t row = c0;
+  if (c1 - c0 != 1) return;  // varlen mode: not a one-query row, the prefill kernel writes it
   uint16_t* ob = p.out + row * p.out_row_stride + (int64_t)hh * kD + d0;
   if (hh >= H) return;
   if (eb == sb) {  // empty (padded) row: defined zeros
@@ -632,6 +610,45 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs p) {
       u32x4{pack_bf16x2(o2[0] * inv, o2[1] * inv), pack_bf16x2(o2[2] * inv, o2[3] * inv),
             pack_bf16x2(o2[4] * inv, o2[5] * inv), pack_bf16x2(o2[6] * inv, o2[7] * inv)};
 }
+
+// Writes the sequences that decode_kernel left as partials, and the zeros of empty rows (in varlen mode only those of
+// one-query sequences; the others belong to the prefill kernel). One workgroup per sequence, thread = (head, 8 dims). Sequence b covers steps [sb, eb) of the layout decode_kernel published in
+// `steps`, with the number G of workgroups it used; workgroup g of G covers [floor(g S / G), floor((g + 1) S / G))
+// (at least one step, as G <= S), and the workgroups touching b, g_first..g_last below, each left a partial at slot
+// b + g. Online rescale over the partials (fp32), the loads of kMergeBatch partials in flight together. Runs after
+// decode_kernel on the same stream, which makes the partials visible.
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs p) {
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  int s_tot = p.steps[p.batch], s_b = p.steps[b], s_e = p.steps[b + 1], s_g = p.steps[p.batch + 1];
+  int c0 = b, c1 = b + 1, slot32 = -1;
+  if (p.cu_q) {
+    c0 = p.cu_q[b];
+    c1 = p.cu_q[b + 1];
+  }
+  if (p.slot_mapping) slot32 = p.slot_mapping[b];
+  // every value in registers here: the loads go out together, one round trip (left to itself the compiler sinks
+  // each load to its first use, behind the branches, one round trip apiece)
+  asm volatile("" ::"s"(s_tot), "s"(s_b), "s"(s_e), "s"(s_g), "s"(c0), "s"(c1), "s"(slot32));
+  // store mode: the new K / V row goes into the cache, now that every read of the split is done; its load is issued
+  // before the merge's and its store made last, so the copy shares the merge's round trip instead of adding its own
+  u32x4 kv_chunk = zero4();
+  uint16_t* kv_dst = nullptr;
+  if (p.slot_mapping) {
+    const int row_elems = p.group ? p.num_heads / p.group * kD : 0;  // HK x 128
+    const int64_t slot = slot32;
+    const int chunk = tid & 127;  // 16-byte chunk of the row: threads 0-127 K, 128-255 V
+    if (slot >= 0 && slot < p.num_blocks * p.block_size && chunk * 8 < row_elems) {
+      const bool is_v = tid >= 128;
+      const uint16_t* src = (is_v ? p.new_v + (int64_t)b * p.new_v_stride : p.new_k + (int64_t)b * p.new_k_stride);
+      kv_dst = const_cast<uint16_t*>(is_v ? p.v_cache : p.k_cache) + slot * row_elems + chunk * 8;
+      kv_chunk = ld_g16(src + chunk * 8);
+    }
+  }
+  merge_row(p, b, tid, s_tot, s_b, s_e, s_g, c0, c1);
+  if (kv_dst) *reinterpret_cast<u32x4*>(kv_dst) = kv_chunk;
+}
+
 
 }  // namespace
 
