@@ -182,8 +182,19 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
     row = q0;
     return q1 - q0 == 1 ? k1 - k0 : 0;
   };
-  int row_first = 0;
-  const int ctx_first = tid < p.batch ? seq_of(tid, row_first) : 0;
+  // the first kThreads sequences' lengths and slots: loaded here, used after the table loads below are issued
+  int l0 = 0, l1 = 0, l2 = 0, l3 = 0, slot_first = -1;
+  if (tid < p.batch) {
+    if (varlen) {
+      l0 = p.cu_q[tid];
+      l1 = p.cu_q[tid + 1];
+      l2 = p.cu_k[tid];
+      l3 = p.cu_k[tid + 1];
+    } else {
+      l2 = p.context_lens[tid];
+    }
+    if (p.slot_mapping) slot_first = p.slot_mapping[tid];
+  }
   if constexpr (BTL) {
     constexpr int kPer = (kBtLds + kThreads - 1) / kThreads;  // entries per thread at most
     const int nbt = p.batch * mb;
@@ -206,6 +217,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
     for (int j = 0; j < kPer; ++j)
       if (tid + j * kThreads < nbt) s_bt[tid + j * kThreads] = vals[j];
   }
+  const int row_first = varlen ? l0 : tid;
+  const int ctx_first = !varlen ? l2 : (l1 - l0 == 1 ? l3 - l2 : 0);
   int run = 0;
   int nmax = 0;  // most steps of one sequence
   for (int base = 0; base < p.batch; base += kThreads) {
@@ -232,7 +245,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
     }
     if (bb < p.batch) {
       s_ctx[bb] = ctx;
-      if (p.slot_mapping) s_snew[bb] = p.slot_mapping[bb];
+      if (p.slot_mapping) s_snew[bb] = base == 0 ? slot_first : p.slot_mapping[bb];
       s_row[bb] = row;
       s_start[bb] = run + before + incl - n;
     }
