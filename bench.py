@@ -333,18 +333,33 @@ def bench_ceiling(dev, w):
                                           ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     sink = torch.empty(1024, dtype=torch.uint8, device=dev)
     region = decode_bytes(w.lens) // 4096 * 4096
-    regions = 7
+    regions = 14  # 2.4 GB: neither one region nor the rotation fits the 256 MB Infinity Cache
     buf = torch.empty(region * regions, dtype=torch.uint8, device=dev)
     buf.fill_(1)
     out = {"stream_read": {}, "decode_pattern_read": {}}
     for grid in (256, 1024, 2048):
+        # 28 back-to-back launches of one layer's bytes (as many as a decode step has calls), rotating regions
         def run(grid=grid):
-            for r in range(regions):
-                assert probe.vox_probe_stream_read(buf.data_ptr() + r * region, region, sink.data_ptr(), grid,
-                                                   _lib.stream_handle(dev)) == 0
+            for r in range(w.LAYERS):
+                assert probe.vox_probe_stream_read(buf.data_ptr() + (r % regions) * region, region, sink.data_ptr(),
+                                                   grid, _lib.stream_handle(dev)) == 0
 
-        ms = _graph_ms(run, 20) / regions
+        ms = _graph_ms(run, 10) / w.LAYERS
         out["stream_read"][f"grid{grid}"] = round(region / (ms * 1e-3) / 1e9, 1)
+    out["stream_read_launch_bytes"] = region
+    # the sustained rate: one launch over the whole 2.4 GB, so its start and end cost little against its length;
+    # what separates it from the per-layer launches above is each launch's ramp and tail
+    sustained = {}
+    for grid in (1024, 2048, 4096):
+        def run_all(grid=grid):
+            assert probe.vox_probe_stream_read(buf.data_ptr(), region * regions, sink.data_ptr(), grid,
+                                               _lib.stream_handle(dev)) == 0
+
+        ms = _graph_ms(run_all, 5)
+        sustained[f"grid{grid}"] = round(region * regions / (ms * 1e-3) / 1e9, 1)
+    out["stream_read_sustained"] = sustained
+    out["stream_read_sustained_bytes"] = region * regions
+    out["stream_read_sustained_gbs"] = max(sustained.values())
     del buf
     # tile offsets of the decode workload: 16-token tiles of every sequence, sequence by sequence
     offs = []
@@ -447,6 +462,39 @@ def bench_prefill(dev):
     tfp = flops / (msp * 1e-3) / 1e12
     out["config2_paged"] = dict(launch_us=round(msp * 1e3, 2), tflops=round(tfp, 2),
                                 pct_mfma_peak=round(100 * tfp / MFMA_BF16_PEAK_TFLOPS, 2), input_sets=PSETS)
+    # the whole config-2 step as BASELINE defines it: Attention.forward stores the step's K/V rows at their slots
+    # (256-token blocks of the shuffled pool) and then attends, over the packed rows (no cached prefix: block_tables
+    # None) or through the block tables (prefix-cache mode, the keys read back from the pool just written);
+    # reference nanovllm_voxcpm/model/layers.py:332-348
+    from voxcpm2_arabic_dialects_turbo_amd.context import reset_context, set_context
+    from voxcpm2_arabic_dialects_turbo_amd.layers import Attention
+
+    layer = Attention(H, D, SCALE, HK)
+    pslots = []
+    for s in range(PSETS):
+        tb = ptables[s].cpu()
+        pslots.append(torch.tensor([int(tb[b, j // BS]) * BS + j % BS for b, n in enumerate(lens) for j in range(n)],
+                                   dtype=torch.int32, device=dev))
+
+    def run_c2_step(paged):
+        def fn():
+            for i in range(PSETS * PREPS):
+                s = i % PSETS
+                layer.k_cache, layer.v_cache = kvp[s, 0], kvp[s, 1]
+                set_context(True, cu, cu, max(lens), max(lens), pslots[s], None, ptables[s] if paged else None)
+                q, k, v = qkv[i % n_sets].split([H * D, HK * D, HK * D], dim=-1)
+                layer(q.view(T, H, D), k.view(T, HK, D), v.view(T, HK, D))
+        return fn
+
+    try:
+        for key, paged in (("config2", False), ("config2_paged", True)):
+            mss = _graph_ms(run_c2_step(paged), 20) / (PSETS * PREPS)
+            out[key]["step_us"] = round(mss * 1e3, 2)
+            out[key]["step_what"] = ("Attention.forward: store_kvcache of the step's K/V rows, then the varlen "
+                                     "causal prefill " + ("through the block tables" if paged else
+                                                          "over the packed rows"))
+    finally:
+        reset_context()
     del qkv, kvp
     # supplementary compute-bound shape: 16 sequences x 2048 tokens, causal
     L, NB = 2048, 16
@@ -641,6 +689,18 @@ def cpu_config1(budget_s: float = 3.0):
                 sample="BASELINE config 1: oracle decode, 1 seq x ctx 512, fp32, torch on CPU")
 
 
+def _cpu_model() -> str:
+    """The host CPU's model name (lscpu's "Model name", from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(w, budget_s: float):
     """The oracle's torch path (fp32, as the reference's tests compute it) on the host cores over a bounded sample of
     the same decode step: layer after layer (store + decode of 150 sequences) until the budget is spent; plus
@@ -649,6 +709,11 @@ def cpu_baseline(w, budget_s: float):
 
     from oracle import attention as ref
 
+    # every core this process may run on (os.cpu_count() counts the whole host, which a container's CPU share can
+    # be far below; both are recorded)
+    cpu_count = os.cpu_count() or 1
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else cpu_count
+    torch.set_num_threads(usable)
     threads = torch.get_num_threads()
     lens = w.lens
     tables = [t.block_table + [-1] * (8 - len(t.block_table)) for t in w.tasks]
@@ -664,6 +729,7 @@ def cpu_baseline(w, budget_s: float):
         done += 1
     nbytes = done * (decode_bytes(lens) + store_bytes(len(lens)))
     return dict(value=round(nbytes / spent / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+                cpu_count=cpu_count, affinity_cpus=usable, threads=threads, cpu_model=_cpu_model(),
                 sample=f"{done} of 28 layers of the config-4 decode step (store + decode, 150 sequences), "
                        f"torch fp32 on CPU, {spent:.1f} s",
                 ms_per_step_extrapolated=round(spent / done * 28 * 1e3, 1),

@@ -135,7 +135,9 @@ size_t vox_prefill_workspace_bytes(int batch);
  *   out_scale[t] = amax / 127,   out_q[t, c] = rint(x[c] / out_scale[t])  (round half to even, int8).
  *   out_q      int8 [T, num_heads * head_dim], token rows out_q_row_stride apart (multiple of 4, 4-byte aligned)
  *   out_scale  fp32 [T]
- *   num_tokens T, the query rows (cu_seqlens_q[batch], or batch * uniform_seqlen_q)
+ *   num_tokens T, the query rows (cu_seqlens_q[batch], or batch * uniform_seqlen_q) that out_q, out_scale and
+ *              the workspace hold; rows at or past it are neither read nor written, so a cu_seqlens_q reaching past
+ *              it truncates the output instead of writing out of bounds (0: nothing to do)
  *   workspace  NULL, or >= vox_prefill_int8_workspace_bytes(...) bytes of scratch (16-byte aligned): where that is
  *              nonzero the call runs as two passes (the bf16 kernel into the workspace, then a per-token
  *              quantization of its rows), which is faster for long sequences whose work items outnumber the CUs;

@@ -228,6 +228,30 @@ def test_decode_stores_and_attends_in_one_call_with_an_unsqueezed_output(monkeyp
     assert o.shape == (2, 1, 16, 128)
 
 
+@pytest.mark.parametrize("layout", ["unaligned_rows", "odd_row_stride", "slot_count"])
+def test_decode_rows_the_fused_store_cannot_read_take_store_then_decode(monkeypatch, layout):
+    """The fused store reads the new rows with 16-byte loads: rows that are not 16-byte aligned or whose stride is not
+    a multiple of 8 elements, and a slot_mapping that is not one slot per row, take store_kvcache and then the
+    decode kernel instead (the reference accepts them: nanovllm_voxcpm/model/layers.py:290-305)."""
+    rec = _Recorder(monkeypatch)
+    attn = Attention(16, 128, 0.125, 2)
+    attn.k_cache, attn.v_cache = torch.zeros(2, 256, 2, 128), torch.zeros(2, 256, 2, 128)
+    lens, bt = torch.tensor([7, 9], dtype=torch.int32), torch.tensor([[0], [1]], dtype=torch.int32)
+    slots = torch.tensor([6, 264], dtype=torch.int32)
+    k = v = torch.zeros(2, 2, 128)
+    if layout == "unaligned_rows":
+        k = torch.zeros(2 * 256 + 1)[1:].view(2, 2, 128)
+    elif layout == "odd_row_stride":
+        v = torch.zeros(2, 2 * 128 + 3)[:, :256].view(2, 2, 128)
+    else:
+        slots = torch.tensor([6, 264, -1], dtype=torch.int32)
+    set_context(False, slot_mapping=slots, context_lens=lens, block_tables=bt)
+    o = attn(torch.zeros(2, 16, 128), k, v)
+    assert [c[0] for c in rec.calls] == ["store_kvcache", "flash_attn_with_kvcache"]
+    assert rec.calls[0][1][0] is k and rec.calls[0][1][1] is v and rec.calls[0][1][4] is slots
+    assert o == "o"
+
+
 def test_decode_without_caches_calls_the_kvcache_kernel_with_an_unsqueezed_query(monkeypatch):
     rec = _Recorder(monkeypatch)
     attn = Attention(16, 128, 0.125, 2)

@@ -426,7 +426,7 @@ int vox_prefill_attn_int8(const void* q, int64_t q_row_stride, const void* key, 
                           void* workspace, size_t workspace_bytes, void* stream) {
   if (batch < 0 || max_seqlen_q < 0 || num_tokens < 0)
     return fail(VOX_EINVAL, "prefill_attn_int8: negative batch, max_seqlen_q or num_tokens");
-  if (batch == 0 || max_seqlen_q == 0) return VOX_OK;
+  if (batch == 0 || max_seqlen_q == 0 || num_tokens == 0) return VOX_OK;
   if (!out_q || !out_scale) return fail(VOX_EINVAL, "prefill_attn_int8: null out_q or out_scale");
   if (num_kv_heads != 1 && num_kv_heads != 2)
     return fail(VOX_EINVAL, "prefill_attn_int8: num_kv_heads %d unsupported (1 or 2)", num_kv_heads);
@@ -442,6 +442,9 @@ int vox_prefill_attn_int8(const void* q, int64_t q_row_stride, const void* key, 
   if (st != VOX_OK) return st;
   if (!cu_seqlens_q && num_tokens != (int64_t)batch * uniform_seqlen_q)
     return fail(VOX_EINVAL, "prefill_attn_int8: num_tokens %lld != batch x uniform_seqlen_q", (long long)num_tokens);
+  // rows at or past num_tokens are never read or written, whatever cu_seqlens_q (device memory the host cannot
+  // check here) says: the outputs and the two-pass scratch are sized by num_tokens
+  a.row_limit = num_tokens;
   const size_t need = workspace ? vox_prefill_int8_workspace_bytes(num_tokens, batch, max_seqlen_q, num_heads,
                                                                    num_kv_heads, head_dim, causal)
                                 : 0;

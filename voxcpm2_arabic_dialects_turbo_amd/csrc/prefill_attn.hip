@@ -139,7 +139,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
     const int h = g * G + rho % G;
     tq_of[rt] = tq;
     h_of[rt] = h;
-    row_ok[rt] = tq < nq;
+    row_ok[rt] = tq < nq && (p.row_limit <= 0 || (int64_t)q0 + tq < p.row_limit);
     qpos[rt] = nk - nq + tq;
     const uint16_t* qp = p.q + (int64_t)(q0 + tq) * p.q_row_stride + (int64_t)h * kD + jq * 8;
 #pragma unroll
@@ -616,7 +616,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
         *reinterpret_cast<uint32_t*>(op + dt * 16) = packed;
       }
     }
-    if (threadIdx.x < (unsigned)BQ && qt * BQ + (int)threadIdx.x < nq)
+    if (threadIdx.x < (unsigned)BQ && qt * BQ + (int)threadIdx.x < nq &&
+        (p.row_limit <= 0 || (int64_t)q0 + qt * BQ + (int)threadIdx.x < p.row_limit))
       p.out_scale[q0 + qt * BQ + threadIdx.x] = fmaxf(__uint_as_float(s_amax[threadIdx.x]), 1e-6f) / 127.f;
     return;
   }

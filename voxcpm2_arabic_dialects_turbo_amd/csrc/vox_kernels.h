@@ -88,6 +88,8 @@ struct PrefillArgs {
   int skip_single;            // sequences with exactly one query are left to the decode kernel (varlen mode)
   int persistent;             // set by the launcher: a fixed grid loops over the (q tile, kv head) items of the
                               // sequences, found by a scan of cu_q (at most kMaxSeqPerLaunch sequences per launch)
+  int64_t row_limit;          // > 0: output rows at or past it are neither read (q) nor written (the rows the caller's
+                              // output holds; a cu_seqlens_q reaching past it truncates instead of writing out of bounds)
 };
 
 struct CopyArgs {

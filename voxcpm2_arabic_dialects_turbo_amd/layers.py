@@ -28,6 +28,22 @@ from .ops import decode_attention, flash_attn_func, flash_attn_varlen_func, flas
 __all__ = ["Attention", "store_kvcache"]
 
 
+def _store_rides_in_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, slot_mapping) -> bool:
+    """Whether a decode step's KV store can ride in the decode call (vox_decode_attn_store): one row per sequence
+    and one slot per row, rows 16-byte aligned with heads contiguous and row strides a multiple of 8 elements (the
+    decode kernel reads the new rows with 16-byte loads). Any other layout takes store_kvcache, whose element path
+    copies unaligned rows, followed by the decode kernel: the same result."""
+    if slot_mapping is None or k.dim() != 3 or v.dim() != 3 or k.shape[0] != q.shape[0] or v.shape != k.shape:
+        return False
+    if slot_mapping.numel() != q.shape[0]:
+        return False
+    for t in (k, v):
+        if t.stride(2) != 1 or t.stride(1) != t.shape[2] or t.stride(0) % 8 or t.data_ptr() % 16 \
+                or t.stride(0) < t.shape[1] * t.shape[2]:
+            return False
+    return True
+
+
 class Attention(nn.Module):
 
     def __init__(
@@ -51,8 +67,7 @@ class Attention(nn.Module):
             context = get_context()
             k_cache, v_cache = self.k_cache, self.v_cache
             cached = bool(k_cache.numel() and v_cache.numel())
-            if cached and not context.is_prefill and context.slot_mapping is not None and k.dim() == 3 \
-                    and k.shape[0] == q.shape[0]:
+            if cached and not context.is_prefill and _store_rides_in_decode(q, k, v, context.slot_mapping):
                 # decode step: the store rides in the decode call (one row per sequence, each writing the slot of
                 # its own newest token)
                 return decode_attention(q, k_cache, v_cache, context.context_lens, context.block_tables, self.scale,
