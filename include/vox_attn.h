@@ -19,12 +19,26 @@
 extern "C" {
 #endif
 
-#define VOX_ABI_VERSION 8
+#define VOX_ABI_VERSION 9
 
 #define VOX_OK 0
 #define VOX_EINVAL 1 /* bad argument: shape, stride, alignment or null pointer (reference: the asserts of
                         nanovllm_voxcpm/model/layers.py:299-302 and kernels/prefill_attn.py:107-108) */
 #define VOX_EHIP 2   /* the HIP runtime reported an error at launch */
+
+/* Plan modes of the decode calls (the `plan` argument). The decode layout (how the sequences' tokens are dealt to the
+ * workgroups, and the block id of every tile) depends only on the lengths, the block tables and, in store mode, the
+ * slots, which every layer of one decode step shares. No reference counterpart: the reference likewise builds
+ * per-step metadata once per forward context for all layers (nanovllm_voxcpm/engine/utils.py:53-57).
+ *   VOX_PLAN_NONE    every workgroup scans the lengths and stages the table itself
+ *   VOX_PLAN_RECORD  the same, and the layout is recorded in the workspace
+ *   VOX_PLAN_REUSE   the layout is read from the workspace, where the last VOX_PLAN_RECORD call on it recorded it;
+ *                    the caller guarantees that call had the same batch, context lengths (varlen: cu_seqlens), block
+ *                    tables, slots (store mode: reuse only after a store-mode record) and workgroup count. Parts of
+ *                    the layout a record cannot hold are scanned again. Batches above 512 sequences run unplanned. */
+#define VOX_PLAN_NONE 0
+#define VOX_PLAN_RECORD 1
+#define VOX_PLAN_REUSE 2
 
 const char* vox_last_error(void);
 int vox_abi_version(void);
@@ -47,23 +61,26 @@ int vox_store_kvcache(const void* key, const void* value, int64_t key_row_stride
  *                kernel may stage them all), but entries past ceil(context_lens[b] / block_size) are never used;
  *                an entry inside the context outside [0, num_blocks) masks that block's keys (no weight)
  *   context_lens int32 [batch]; 0 = padded row, whose output is written as zeros
- *   workspace    >= vox_decode_workspace_bytes(batch) bytes of scratch (split-KV partials), used by the two
- *                kernels the call launches in order on `stream`
+ *   plan         VOX_PLAN_NONE, VOX_PLAN_RECORD or VOX_PLAN_REUSE (above)
+ *   workspace    >= vox_decode_workspace_bytes(batch) bytes of scratch, 16-byte aligned: the split-KV partials and
+ *                the step layout the two kernels of the call (launched in order on `stream`) pass on, and the plan
+ *                records. VOX_PLAN_REUSE reads what the recording call left there, so the workspace must be the
+ *                same and untouched by other calls in between; no other contents need to survive a call.
  *   out          bf16 [batch, num_heads, head_dim], contiguous
  * Supported: head_dim 128, num_kv_heads 1 or 2, num_heads <= 16, block_size a multiple of 32. */
 int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
                     int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
                     int max_blocks, const int32_t* context_lens, int batch, int num_heads, int num_kv_heads,
-                    int head_dim, float softmax_scale, void* workspace, size_t workspace_bytes, void* out,
-                    void* stream);
+                    int head_dim, float softmax_scale, int plan, void* workspace, size_t workspace_bytes,
+                    void* out, void* stream);
 
 /* The decode step's KV store and decode attention in one call: vox_store_kvcache(key, value, key_row_stride,
  * value_row_stride, k_cache, v_cache, num_blocks * block_size, slot_mapping, batch, ...) followed by
  * vox_decode_attn(...) (reference: the decode branch of nanovllm_voxcpm/model/layers.py:326-358, store_kvcache then
  * flash_attn_with_kvcache), without the store's own launch: the split kernel reads each sequence's new token from
- * key / value where the tile it loads holds that token's slot, and the merge kernel writes the rows into the caches
- * after every read. Same results as the two calls when no slot_mapping[b] lies inside another sequence's context
- * (the engine's sequences each write only their own last block); slot -1 and slots outside the cache store nothing.
+ * key / value where the tile it loads holds that token's slot, and writes the rows into the caches. Same results as
+ * the two calls when no slot_mapping[b] lies inside another sequence's context (the engine's sequences each write
+ * only their own last block); slot -1 and slots outside the cache store nothing.
  *   key / value    bf16 [batch, num_kv_heads, head_dim], heads contiguous, rows *_row_stride elements apart
  *                  (multiples of 8), 16-byte aligned
  *   slot_mapping   int32 [batch]
@@ -72,7 +89,7 @@ int vox_decode_attn_store(const void* q, int64_t q_row_stride, const void* key, 
                           int64_t key_row_stride, int64_t value_row_stride, const int32_t* slot_mapping,
                           void* k_cache, void* v_cache, int64_t num_blocks, int block_size,
                           const int32_t* block_tables, int64_t bt_stride, int max_blocks, const int32_t* context_lens,
-                          int batch, int num_heads, int num_kv_heads, int head_dim, float softmax_scale,
+                          int batch, int num_heads, int num_kv_heads, int head_dim, float softmax_scale, int plan,
                           void* workspace, size_t workspace_bytes, void* out, void* stream);
 
 /* vox_decode_attn without the workspace argument: the split-KV scratch is a static device array of 16 MiB
@@ -82,13 +99,14 @@ int vox_decode_attn_store(const void* q, int64_t q_row_stride, const void* key, 
  * Returns VOX_EINVAL when vox_decode_workspace_bytes(batch) exceeds the array (not for any batch at the default
  * workgroup count: batches are launched 512 sequences at a time). Every call on one GPU shares that GPU's array:
  * calls that overlap on one GPU (different streams, or host threads) race and must be serialized by the caller.
- * The array needs no clearing: each call writes every scratch value it reads. Other arguments as vox_decode_attn. */
+ * The array needs no clearing: each call writes every scratch value it reads. Runs with VOX_PLAN_NONE. Other
+ * arguments as vox_decode_attn. */
 int vox_decode_attn_noalloc(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
                             int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
                             int max_blocks, const int32_t* context_lens, int batch, int num_heads, int num_kv_heads,
                             int head_dim, float softmax_scale, void* out, void* stream);
 
-/* Scratch bytes vox_decode_attn needs for `batch` sequences on the current device (split-KV partials). No reference
+/* Workspace bytes vox_decode_attn needs for `batch` sequences on the current device. No reference
  * counterpart: flash-attn sizes its split-KV buffers internally (reference call site: nanovllm_voxcpm/model/layers.py:350). */
 size_t vox_decode_workspace_bytes(int batch);
 
@@ -109,18 +127,20 @@ void vox_set_decode_workgroups(int workgroups);
  *   cu_seqlens_q/k int32 [batch + 1]; both NULL selects uniform lengths uniform_seqlen_q / uniform_seqlen_k
  *   causal         bottom-right aligned: query i of a sequence with nq queries and nk keys sees keys j <= nk-nq+i
  *   out            bf16 [T, num_heads, head_dim], token rows out_row_stride apart
- *   workspace      NULL, or >= vox_prefill_workspace_bytes(batch) bytes of scratch: with block tables and
- *                  cu_seqlens, sequences with exactly one query (the decode rows of a mixed prefill + decode step) then
- *                  run on the split-KV decode kernels, which spread long contexts over every CU (needs num_heads <= 16,
- *                  num_kv_heads 1 or 2, block_size a multiple of 32, out 16-byte aligned with out_row_stride a multiple
- *                  of 8; otherwise, or with NULL, the prefill kernel takes every row). Same results either way.
+ *   plan, workspace
+ *                  NULL, or a decode workspace (>= vox_prefill_workspace_bytes(batch) bytes, under vox_decode_attn's
+ *                  contract) and its plan mode: with block tables and cu_seqlens, sequences with exactly one query (the
+ *                  decode rows of a mixed prefill + decode step) then run on the split-KV decode kernel, which spreads
+ *                  long contexts over every CU (needs num_heads <= 16, num_kv_heads 1 or 2, block_size a multiple of
+ *                  32, out 16-byte aligned with out_row_stride a multiple of 8; otherwise, or with NULL, the prefill
+ *                  kernel takes every row). Same results either way.
  * Supported: head_dim 128, num_heads / num_kv_heads dividing 128. */
 int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const void* value,
                      int64_t key_row_stride, int64_t value_row_stride, const void* k_cache, const void* v_cache,
                      int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
                      int max_blocks, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch,
                      int max_seqlen_q, int uniform_seqlen_q, int uniform_seqlen_k, int num_heads, int num_kv_heads,
-                     int head_dim, float softmax_scale, int causal, void* out, int64_t out_row_stride,
+                     int head_dim, float softmax_scale, int causal, void* out, int64_t out_row_stride, int plan,
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /* Scratch bytes vox_prefill_attn's one-query rows need for `batch` sequences on the current device. No reference

@@ -57,7 +57,7 @@ def test_store_rejects_bad_arguments_without_launching():
 def _decode(**over):
     p = ctypes.c_void_p(256)
     a = dict(q=p, qs=16 * 128, kc=p, vc=p, nb=4, bs=256, bt=p, bts=8, mb=8, lens=p, b=2, h=16, hk=2, d=128,
-             scale=0.088, ws=p, wsb=1 << 30, out=p, stream=None)
+             scale=0.088, plan=0, ws=p, wsb=1 << 30, out=p, stream=None)
     a.update(over)
     return _lib.load().vox_decode_attn(*a.values())
 
@@ -67,7 +67,8 @@ def test_decode_rejects_unsupported_shapes():
     for over, msg in [(dict(d=64), "head_dim"), (dict(hk=4, h=16), "num_kv_heads"), (dict(h=32), "num_heads"),
                       (dict(bs=100), "block_size"), (dict(bts=4), "block table"),
                       (dict(wsb=10), "workspace"), (dict(qs=100), "row stride"), (dict(lens=None), "null"),
-                      (dict(scale=float("nan")), "finite")]:
+                      (dict(scale=float("nan")), "finite"), (dict(plan=3), "plan mode"),
+                      (dict(plan=-1), "plan mode")]:
         assert _decode(**over) == _lib.VOX_EINVAL, over
         assert msg in _err(), (over, _err())
 
@@ -75,7 +76,7 @@ def test_decode_rejects_unsupported_shapes():
 def _decode_store(**over):
     p = ctypes.c_void_p(256)
     a = dict(q=p, qs=16 * 128, key=p, value=p, ks=20 * 128, vs=20 * 128, slots=p, kc=p, vc=p, nb=4, bs=256, bt=p, bts=8,
-             mb=8, lens=p, b=2, h=16, hk=2, d=128, scale=0.088, ws=p, wsb=1 << 30, out=p, stream=None)
+             mb=8, lens=p, b=2, h=16, hk=2, d=128, scale=0.088, plan=0, ws=p, wsb=1 << 30, out=p, stream=None)
     a.update(over)
     return _lib.load().vox_decode_attn_store(*a.values())
 
@@ -86,7 +87,8 @@ def test_decode_store_rejects_bad_arguments():
     assert _decode_store(b=0) == _lib.VOX_OK
     for over, msg in [(dict(key=None), "null"), (dict(slots=None), "null"), (dict(ks=100), "key / value"),
                       (dict(vs=128), "key / value"), (dict(value=ctypes.c_void_p(264)), "key / value"),
-                      (dict(d=64), "head_dim"), (dict(wsb=10), "workspace"), (dict(lens=None), "null")]:
+                      (dict(d=64), "head_dim"), (dict(wsb=10), "workspace"), (dict(lens=None), "null"),
+                      (dict(plan=7), "plan mode")]:
         assert _decode_store(**over) == _lib.VOX_EINVAL, over
         assert msg in _err(), (over, _err())
 
@@ -99,7 +101,8 @@ def test_decode_workspace_and_grid_choice():
     def need(b, g):
         up = lambda x: -(-x // 256) * 256
         s = min(b, 512)  # sequences per launch
-        return up((s + g) * (16 * 128 + 32) * 4) + up((s + 2) * 4)
+        # fp32 partials (one per sequence and workgroup), the step layout, plan records (4 KiB per workgroup)
+        return up((s + g) * (16 * 128 + 32) * 4) + up((s + 2) * 4) + up(g * 1024 * 4)
     for b in (1, 40, 150, 512, 5000):
         assert lib.vox_decode_workspace_bytes(b) == need(b, grid)
     lib.vox_set_decode_workgroups(7)
@@ -116,7 +119,7 @@ def test_prefill_rejects_bad_arguments():
     p = ctypes.c_void_p(256)
     # valid apart from the fake pointers: never passed unmodified (it would launch)
     args = [p, 2048, p, p, 256, 256, None, None, 0, 0, None, 0, 0, p, p, 2, 16, 0, 0, 16, 2, 128, 0.088, 1, p, 2048,
-            None, 0, None]
+            0, None, 0, None]
     bad = list(args)
     bad[21] = 64  # head_dim
     assert lib.vox_prefill_attn(*bad) == _lib.VOX_EINVAL and "head_dim" in _err()
@@ -132,8 +135,11 @@ def test_prefill_rejects_bad_arguments():
     paged = list(args)  # paged varlen with a workspace below vox_prefill_workspace_bytes: rejected, no launch
     paged[2:4] = [None, None]
     paged[6:13] = [p, p, 64, 256, p, 8, 8]
-    paged[26:28] = [p, 16]
+    paged[27:29] = [p, 16]
     assert lib.vox_prefill_attn(*paged) == _lib.VOX_EINVAL and "workspace" in _err()
+    paged[27:29] = [p, 1 << 30]
+    paged[26] = 5  # not a plan mode
+    assert lib.vox_prefill_attn(*paged) == _lib.VOX_EINVAL and "plan mode" in _err()
     assert lib.vox_prefill_workspace_bytes(2) == lib.vox_decode_workspace_bytes(2) > 16
     zero = list(args)
     zero[15] = 0  # empty batch: nothing to do
@@ -206,7 +212,7 @@ def test_prefill_with_one_kv_head_for_128_query_heads_returns_a_status(int8):
     import sys
 
     fn = "vox_prefill_attn_int8" if int8 else "vox_prefill_attn"
-    tail = "None, p, 128 * 128, p, 4, None, 0, None" if int8 else "p, 128 * 128, None, 0, None"
+    tail = "None, p, 128 * 128, p, 4, None, 0, None" if int8 else "p, 128 * 128, 0, None, 0, None"
     code = f"""
 import ctypes, sys
 sys.path.insert(0, {os.path.dirname(os.path.dirname(os.path.abspath(__file__)))!r})

@@ -344,3 +344,80 @@ def test_decode_with_the_store_in_a_hip_graph_replays_like_eager():
         torch.cuda.synchronize()
         assert torch.equal(out, want), f"replay {step}: output"
         assert torch.equal(k1, k_ref) and torch.equal(v1, v_ref), f"replay {step}: caches"
+
+
+def _layers_of_one_step(gen, lens, n_layers, bs=BLOCK, store=False, width_extra=0):
+    """n_layers layers of one decode step: shared lengths, tables (and slots), per-layer caches, q (and new rows)."""
+    pool = sum(-(-max(n, 1) // bs) for n in lens) + 4
+    _, _, tables = paged_pool(gen, lens, pool, block_size=bs, extra_cols=width_extra)
+    layers = []
+    for _ in range(n_layers):
+        kc, vc = randn(gen, pool, bs, HK, D), randn(gen, pool, bs, HK, D)
+        qkv = randn(gen, len(lens), (H + 2 * HK) * D).to(DEV)
+        layers.append((kc.to(DEV), vc.to(DEV), qkv))
+    slots = [int(tables[b, (n - 1) // bs]) * bs + (n - 1) % bs if n > 0 else -1 for b, n in enumerate(lens)]
+    return layers, tables.to(DEV), torch.tensor(lens, dtype=torch.int32, device=DEV), \
+        torch.tensor(slots, dtype=torch.int32, device=DEV)
+
+
+def _run_step(layers, tables, lens, slots, plan, store):
+    outs, caches = [], []
+    for kc, vc, qkv in layers:
+        B = qkv.shape[0]
+        q, k, v = qkv.split([H * D, HK * D, HK * D], dim=-1)
+        k1, v1 = kc.clone(), vc.clone()
+        kw = dict(key=k.view(B, HK, D), value=v.view(B, HK, D), slot_mapping=slots) if store else {}
+        outs.append(decode_attention(q.view(B, H, D), k1, v1, lens, tables, SCALE, plan=plan, **kw))
+        caches.append((k1, v1))
+    torch.cuda.synchronize()
+    return outs, caches
+
+
+@pytest.mark.parametrize("store", [False, True])
+def test_plan_recorded_by_the_first_layer_and_reused_by_the_others(store):
+    """A decode step whose plan (the layout: each workgroup's range, sequences and tile block ids) is recorded by
+    the first layer's call and reused by the next ones gives the unplanned calls' outputs bit for bit (and, with the
+    store folded in, the same caches), and every layer matches the oracle."""
+    from voxcpm2_arabic_dialects_turbo_amd import ops
+
+    gen = torch.Generator().manual_seed(150)
+    lens = uniform_lens(gen, 150, 256, 2048)
+    lens[7] = 0
+    layers, tables, lens_d, slots = _layers_of_one_step(gen, lens, 4, store=store)
+    ops.forget_plans()
+    planned, pc = _run_step(layers, tables, lens_d, slots, ("step", 1), store)
+    plain, cc = _run_step(layers, tables, lens_d, slots, None, store)
+    for i in range(len(layers)):
+        assert torch.equal(planned[i], plain[i]), f"layer {i}: planned call differs from the unplanned one"
+        assert torch.equal(pc[i][0], cc[i][0]) and torch.equal(pc[i][1], cc[i][1])
+    kc, vc, qkv = layers[2]
+    q, k, v = qkv.split([H * D, HK * D, HK * D], dim=-1)
+    kc2, vc2 = kc.cpu(), vc.cpu()
+    if store:
+        ref.store_kvcache(k.view(-1, HK, D).cpu(), v.view(-1, HK, D).cpu(), kc2, vc2, slots.cpu())
+    attn_close(planned[2], ref.decode(q.view(-1, H, D).float().cpu(), kc2, vc2, lens, tables.cpu(), SCALE),
+               "planned layer 2")
+
+
+@pytest.mark.parametrize("grid, lens", [(2, [700] * 60), (1, [40] * 100 + [3000]), (5, [1] * 300 + [2048] * 3)],
+                         ids=["range_beyond_a_record", "window_beyond_64_sequences", "many_rounds"])
+def test_plan_records_that_cannot_hold_a_range_fall_back_to_the_scan(grid, lens):
+    """Ranges longer than a record holds, or touching more than the 64 sequences of its window, are recorded as
+    unusable; reusing the plan then scans the layout again in those workgroups: same bits as unplanned calls."""
+    from voxcpm2_arabic_dialects_turbo_amd import ops
+
+    lib = _lib.load()
+    lib.vox_set_decode_workgroups(grid)
+    try:
+        gen = torch.Generator().manual_seed(151)
+        layers, tables, lens_d, slots = _layers_of_one_step(gen, lens, 3)
+        ops.forget_plans()
+        planned, _ = _run_step(layers, tables, lens_d, slots, ("fallback", grid), False)
+        plain, _ = _run_step(layers, tables, lens_d, slots, None, False)
+    finally:
+        lib.vox_set_decode_workgroups(0)
+    for i in range(len(layers)):
+        assert torch.equal(planned[i], plain[i]), f"layer {i}"
+    kc, vc, qkv = layers[1]
+    attn_close(planned[1], ref.decode(qkv[:, :H * D].view(-1, H, D).float().cpu(), kc.cpu(), vc.cpu(), lens,
+                                      tables.cpu(), SCALE), "fallback layer 1")

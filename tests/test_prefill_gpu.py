@@ -463,10 +463,10 @@ def test_varlen_one_query_rows_run_on_the_decode_kernels():
 
 
 def test_mixed_step_captured_in_a_hip_graph_replays_like_eager():
-    """A mixed prefill + decode varlen call runs its decode rows on the caller's stream and its prefill rows on the
-    library's second stream (event fork and join). Captured in a HIP graph and replayed four times, with eager calls on
-    other inputs between the replays, every replay equals the eager result bit for bit, which is within tolerance of
-    the oracle."""
+    """A mixed prefill + decode varlen call runs on the caller's stream: the persistent prefill grid over the
+    multi-query rows, then the decode kernel (and its merge kernel) over the one-query rows. Captured in a HIP graph and
+    replayed four times, with eager calls on other inputs between the replays, every replay equals the eager result
+    bit for bit, which is within tolerance of the oracle."""
     gen = torch.Generator().manual_seed(91)
     pre, dec = [300, 450, 77], [700, 130, 1500, 2, 999]
     nk, nq = pre + dec, pre + [1] * len(dec)

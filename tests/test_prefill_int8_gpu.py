@@ -241,3 +241,67 @@ def test_int8_two_pass_with_uniform_lengths():
                            quant=True, inv_smooth=inv.to(DEV))
     cu = torch.arange(0, B * L + 1, L, dtype=torch.int32)
     _check(out, ref.varlen(q.float(), cu, cu, k=k, v=v), "uniform two-pass int8", inv)
+
+
+def test_int8_two_pass_and_fused_forms_agree_on_one_shape(monkeypatch):
+    """The two forms of the int8 output on the same inputs: the two-pass form quantizes the bf16-rounded o (as the
+    reference's flash-attn + quantize path does), the fused epilogue the fp32 o (as the reference's Triton QUANT
+    epilogue does, kernels/prefill_attn.py:84-92). Which one runs depends on the shape and the CU count, so they must
+    agree: scales within bf16 rounding of the row maximum (relative 2^-8) and codes within one step."""
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(83)
+    lens = [333, 150, 271, 500, 9, 310]
+    T = sum(lens)
+    assert lib.vox_prefill_int8_workspace_bytes(T, len(lens), max(lens), H, HK, D, 1) > 0
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device=DEV)
+    q, k, v = (randn(gen, T, n, D).to(DEV) for n in (H, HK, HK))
+    inv = (torch.rand(H * D, generator=gen) + 0.5).to(DEV)
+
+    def run():
+        return varlen_attention(q, k, v, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=max(lens),
+                                softmax_scale=SCALE, causal=True, quant=True, inv_smooth=inv)
+
+    q2, s2 = run()
+    monkeypatch.setattr(lib, "vox_prefill_int8_workspace_bytes", lambda *a: 0)
+    q1, s1 = run()
+    torch.cuda.synchronize()
+    rel = ((s1 - s2).abs() / s1).max().item()
+    assert rel <= 2.0 ** -8, f"scales of the two forms differ by {rel:.3g} (relative)"
+    step = (q1.int() - q2.int()).abs().max().item()
+    assert step <= 1, f"codes of the two forms differ by {step} steps"
+
+
+@pytest.mark.parametrize("two_pass", [True, False])
+def test_int8_output_rows_past_num_tokens_are_never_written(two_pass, monkeypatch):
+    """A caller whose num_tokens is below cu_seqlens_q[batch] (the library cannot read device memory to check) gets
+    the rows below num_tokens computed and nothing written past them: the guard bytes after out_q, out_scale and the
+    two-pass scratch stay as they were."""
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(84)
+    lens = [400, 390, 380, 370, 360, 350]
+    T = sum(lens)
+    cut = T - 500  # the caller's num_tokens: the last sequences' rows fall past it
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device=DEV)
+    q, k, v = (randn(gen, T, n, D).to(DEV) for n in (H, HK, HK))
+    guard = 4096
+    out_q = torch.full((cut * H * D + guard,), 77, dtype=torch.int8, device=DEV)
+    out_s = torch.full((cut + guard,), 7.0, dtype=torch.float32, device=DEV)
+    ws_bytes = lib.vox_prefill_int8_workspace_bytes(cut, len(lens), max(lens), H, HK, D, 1) if two_pass else 0
+    assert (ws_bytes > 0) == two_pass
+    ws = torch.full((ws_bytes + guard,), 0x5A, dtype=torch.uint8, device=DEV)
+    st = lib.vox_prefill_attn_int8(q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(), k.stride(0), v.stride(0),
+                                   None, None, 0, 0, None, 0, 0, cu.data_ptr(), cu.data_ptr(), len(lens), max(lens), 0,
+                                   0, H, HK, D, SCALE, 1, None, out_q.data_ptr(), H * D, out_s.data_ptr(), cut,
+                                   ws.data_ptr() if two_pass else None, ws_bytes, _lib.stream_handle(q.device))
+    _lib.check(st, "prefill_attn_int8")
+    torch.cuda.synchronize()
+    assert bool((out_q[cut * H * D:] == 77).all()), "int8 rows written past num_tokens"
+    assert bool((out_s[cut:] == 7.0).all()), "scales written past num_tokens"
+    assert bool((ws[ws_bytes:] == 0x5A).all()), "two-pass scratch written past num_tokens rows"
+    full_q, full_s = varlen_attention(q, k, v, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=max(lens),
+                                      softmax_scale=SCALE, causal=True, quant=True)
+    if not two_pass:  # (the full call takes the two-pass form for this shape)
+        monkeypatch.setattr(lib, "vox_prefill_int8_workspace_bytes", lambda *a: 0)
+        full_q, full_s = varlen_attention(q, k, v, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=max(lens),
+                                          softmax_scale=SCALE, causal=True, quant=True)
+    assert torch.equal(out_q[:cut * H * D].view(cut, H * D), full_q[:cut]) and torch.equal(out_s[:cut], full_s[:cut])

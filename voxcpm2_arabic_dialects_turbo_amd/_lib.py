@@ -17,7 +17,9 @@ import torch  # noqa: F401  (must be loaded before the library: shared HIP runti
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvoxattn.so")
 
 VOX_OK, VOX_EINVAL, VOX_EHIP = 0, 1, 2
-ABI_VERSION = 8
+ABI_VERSION = 9
+
+PLAN_NONE, PLAN_RECORD, PLAN_REUSE = 0, 1, 2
 
 # every symbol include/vox_attn.h declares
 EXPORTS = (
@@ -45,10 +47,11 @@ _SIGNATURES = {
     "vox_store_kvcache": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _i64,
                                  _i32, _i32, _c_void_p]),
     "vox_decode_attn": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _i64, _i32,
-                               _c_void_p, _i32, _i32, _i32, _i32, _f32, _c_void_p, _size, _c_void_p, _c_void_p]),
+                               _c_void_p, _i32, _i32, _i32, _i32, _f32, _i32, _c_void_p, _size, _c_void_p,
+                               _c_void_p]),
     "vox_decode_attn_store": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p,
                                      _c_void_p, _i64, _i32, _c_void_p, _i64, _i32, _c_void_p, _i32, _i32, _i32, _i32,
-                                     _f32, _c_void_p, _size, _c_void_p, _c_void_p]),
+                                     _f32, _i32, _c_void_p, _size, _c_void_p, _c_void_p]),
     "vox_decode_attn_noalloc": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _i64, _i32,
                                        _c_void_p, _i32, _i32, _i32, _i32, _f32, _c_void_p, _c_void_p]),
     "vox_decode_workspace_bytes": (_size, [_i32]),
@@ -56,7 +59,7 @@ _SIGNATURES = {
     "vox_set_decode_workgroups": (None, [_i32]),
     "vox_prefill_attn": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64,
                                 _i32, _c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32,
-                                _i32, _i32, _f32, _i32, _c_void_p, _i64, _c_void_p, _size, _c_void_p]),
+                                _i32, _i32, _f32, _i32, _c_void_p, _i64, _i32, _c_void_p, _size, _c_void_p]),
     "vox_prefill_workspace_bytes": (_size, [_i32]),
     "vox_copy_kv_block_prefix": (_i32, [_c_void_p, _i64, _i64, _i32, _i64, _i32, _c_void_p, _i32, _i32, _c_void_p]),
     "vox_prefill_attn_int8": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64,
@@ -110,6 +113,24 @@ def check(status: int, what: str) -> None:
 def stream_handle(device: torch.device) -> int:
     """The hipStream_t of torch's current stream on ``device`` (0 = null stream)."""
     return torch.cuda.current_stream(device).cuda_stream
+
+
+_capture_info = None
+
+
+def capture_id(stream: int) -> int:
+    """The id of the HIP graph capture in progress on ``stream``, 0 when it is not capturing
+    (hipStreamGetCaptureInfo of the HIP runtime libvoxattn.so is linked against)."""
+    global _capture_info
+    if _capture_info is None:
+        fn = load().hipStreamGetCaptureInfo
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_ulonglong)]
+        _capture_info = fn
+    status, ident = ctypes.c_int(0), ctypes.c_ulonglong(0)
+    if _capture_info(stream, ctypes.byref(status), ctypes.byref(ident)) != 0:
+        raise VoxAttnError("hipStreamGetCaptureInfo failed")
+    return int(ident.value) if status.value == 1 else 0  # hipStreamCaptureStatusActive
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

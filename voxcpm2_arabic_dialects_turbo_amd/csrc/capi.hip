@@ -79,29 +79,44 @@ int vox_decode_workgroups(void) {
 void vox_set_decode_workgroups(int workgroups) { g_decode_grid_override = workgroups > 0 ? workgroups : 0; }
 
 namespace {
-// Workspace of one decode launch of `slice` sequences: fp32 partials [slice + grid] then the int32 step layout
-// [slice + 2] (first step of every sequence, the total, the active workgroup count), each 256-byte aligned.
-size_t decode_partials_bytes(int slice, int grid) {
-  return ((size_t)(slice + grid) * vox::kPartialFloats * sizeof(float) + 255) / 256 * 256;
+// Workspace of decode launches of up to `slice` sequences over `grid` workgroups, each part 256-byte aligned: the fp32
+// split-KV partials [slice + grid][kPartialFloats], the int32 step layout [slice + 2] (first step of every sequence,
+// the total, the active workgroup count) that the merge kernel reads, then the plan records [grid][kPlanRecInts].
+struct DecodeWorkspace {
+  size_t partials, steps, plan, total;
+};
+size_t round256(size_t n) { return (n + 255) / 256 * 256; }
+DecodeWorkspace decode_workspace(int slice, int grid) {
+  DecodeWorkspace w;
+  w.partials = 0;
+  w.steps = round256((size_t)(slice + grid) * vox::kPartialFloats * 4);
+  w.plan = w.steps + round256((size_t)(slice + 2) * 4);
+  w.total = w.plan + round256((size_t)grid * vox::kPlanRecInts * 4);
+  return w;
 }
 }  // namespace
 
 size_t vox_decode_workspace_bytes(int batch) {
   if (batch <= 0) return 0;
   const int slice = batch < vox::kMaxSeqPerLaunch ? batch : vox::kMaxSeqPerLaunch;
-  return decode_partials_bytes(slice, vox_decode_workgroups()) + ((size_t)(slice + 2) * 4 + 255) / 256 * 256;
+  return decode_workspace(slice, vox_decode_workgroups()).total;
 }
 
 }  // extern "C"
 
 namespace {
-// Launches the split and merge kernels over `batch` sequences in slices of kMaxSeqPerLaunch (each slice's step
-// layout lives in LDS), all sharing the workspace; `a` describes the whole batch.
-int launch_decode_slices(const vox::DecodeArgs& a, int batch, int num_kv_heads, void* workspace, hipStream_t stream) {
+// Launches the decode kernel over `batch` sequences in slices of kMaxSeqPerLaunch (each slice's step layout lives
+// in LDS), all sharing the workspace; `a` describes the whole batch. A call of several slices runs unplanned (the
+// workspace holds one plan).
+int launch_decode_slices(const vox::DecodeArgs& a, int batch, int num_kv_heads, int plan, void* workspace,
+                         hipStream_t stream) {
   const int slice_max = batch < vox::kMaxSeqPerLaunch ? batch : vox::kMaxSeqPerLaunch;
+  const DecodeWorkspace ws = decode_workspace(slice_max, a.grid);
   vox::DecodeArgs base = a;
-  base.partials = (float*)workspace;
-  base.steps = (int32_t*)((char*)workspace + decode_partials_bytes(slice_max, a.grid));
+  base.partials = (float*)((char*)workspace + ws.partials);
+  base.steps = (int32_t*)((char*)workspace + ws.steps);
+  base.plan = (int32_t*)((char*)workspace + ws.plan);
+  base.plan_mode = batch <= vox::kMaxSeqPerLaunch ? plan : vox::kPlanNone;
   for (int b0 = 0; b0 < batch; b0 += vox::kMaxSeqPerLaunch) {
     vox::DecodeArgs s = base;
     s.batch = batch - b0 < vox::kMaxSeqPerLaunch ? batch - b0 : vox::kMaxSeqPerLaunch;
@@ -186,9 +201,11 @@ extern "C" {
 int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
                     int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
                     int max_blocks, const int32_t* context_lens, int batch, int num_heads, int num_kv_heads,
-                    int head_dim, float softmax_scale, void* workspace, size_t workspace_bytes, void* out,
-                    void* stream) {
+                    int head_dim, float softmax_scale, int plan, void* workspace, size_t workspace_bytes,
+                    void* out, void* stream) {
   if (batch < 0) return fail(VOX_EINVAL, "decode_attn: batch < 0");
+  if (plan != VOX_PLAN_NONE && plan != VOX_PLAN_RECORD && plan != VOX_PLAN_REUSE)
+    return fail(VOX_EINVAL, "decode_attn: plan mode %d", plan);
   if (batch == 0) return VOX_OK;
   vox::DecodeArgs a;
   const int st = decode_setup(q, q_row_stride, k_cache, v_cache, num_blocks, block_size, block_tables, bt_stride,
@@ -196,16 +213,18 @@ int vox_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, co
                               workspace, workspace_bytes, out, &a);
   if (st != VOX_OK) return st;
   // batches beyond one launch's LDS step layout run as consecutive launches on the stream (shared workspace)
-  return launch_decode_slices(a, batch, num_kv_heads, workspace, (hipStream_t)stream);
+  return launch_decode_slices(a, batch, num_kv_heads, plan, workspace, (hipStream_t)stream);
 }
 
 int vox_decode_attn_store(const void* q, int64_t q_row_stride, const void* key, const void* value,
                           int64_t key_row_stride, int64_t value_row_stride, const int32_t* slot_mapping,
                           void* k_cache, void* v_cache, int64_t num_blocks, int block_size,
                           const int32_t* block_tables, int64_t bt_stride, int max_blocks, const int32_t* context_lens,
-                          int batch, int num_heads, int num_kv_heads, int head_dim, float softmax_scale,
+                          int batch, int num_heads, int num_kv_heads, int head_dim, float softmax_scale, int plan,
                           void* workspace, size_t workspace_bytes, void* out, void* stream) {
   if (batch < 0) return fail(VOX_EINVAL, "decode_attn_store: batch < 0");
+  if (plan != VOX_PLAN_NONE && plan != VOX_PLAN_RECORD && plan != VOX_PLAN_REUSE)
+    return fail(VOX_EINVAL, "decode_attn_store: plan mode %d", plan);
   if (batch == 0) return VOX_OK;
   if (!key || !value || !slot_mapping) return fail(VOX_EINVAL, "decode_attn_store: null key, value or slot_mapping");
   const int64_t row = (int64_t)num_kv_heads * head_dim;
@@ -223,7 +242,7 @@ int vox_decode_attn_store(const void* q, int64_t q_row_stride, const void* key, 
   a.new_v = (const uint16_t*)value;
   a.new_k_stride = key_row_stride;
   a.new_v_stride = value_row_stride;
-  return launch_decode_slices(a, batch, num_kv_heads, workspace, (hipStream_t)stream);
+  return launch_decode_slices(a, batch, num_kv_heads, plan, workspace, (hipStream_t)stream);
 }
 
 size_t vox_prefill_workspace_bytes(int batch) { return vox_decode_workspace_bytes(batch); }
@@ -282,8 +301,8 @@ int vox_decode_attn_noalloc(const void* q, int64_t q_row_stride, const void* k_c
   void* ws = scratch_on_current_device();
   if (!ws) return VOX_EHIP;
   return vox_decode_attn(q, q_row_stride, k_cache, v_cache, num_blocks, block_size, block_tables, bt_stride,
-                         max_blocks, context_lens, batch, num_heads, num_kv_heads, head_dim, softmax_scale, ws,
-                         kScratchBytes, out, stream);
+                         max_blocks, context_lens, batch, num_heads, num_kv_heads, head_dim, softmax_scale,
+                         VOX_PLAN_NONE, ws, kScratchBytes, out, stream);
 }
 
 }  // extern "C"
@@ -359,7 +378,7 @@ int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const
                      int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
                      int max_blocks, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch,
                      int max_seqlen_q, int uniform_seqlen_q, int uniform_seqlen_k, int num_heads, int num_kv_heads,
-                     int head_dim, float softmax_scale, int causal, void* out, int64_t out_row_stride,
+                     int head_dim, float softmax_scale, int causal, void* out, int64_t out_row_stride, int plan,
                      void* workspace, size_t workspace_bytes, void* stream) {
   if (batch < 0 || max_seqlen_q < 0) return fail(VOX_EINVAL, "prefill_attn: negative batch or max_seqlen_q");
   if (batch == 0 || max_seqlen_q == 0) return VOX_OK;
@@ -384,8 +403,11 @@ int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const
                            ((uintptr_t)out & 15u) == 0;
   if (decode_rows) {
     const size_t need = vox_prefill_workspace_bytes(batch);
-    if (workspace_bytes < need)
-      return fail(VOX_EINVAL, "prefill_attn: workspace of %zu bytes, %zu needed", workspace_bytes, need);
+    if (workspace_bytes < need || !aligned16(workspace))
+      return fail(VOX_EINVAL, "prefill_attn: workspace of %zu bytes (16-byte aligned), %zu needed", workspace_bytes,
+                  need);
+    if (plan != VOX_PLAN_NONE && plan != VOX_PLAN_RECORD && plan != VOX_PLAN_REUSE)
+      return fail(VOX_EINVAL, "prefill_attn: plan mode %d", plan);
     a.skip_single = 1;
     a.persistent = 1;  // the (q tile, sequence) grid would be mostly the decode rows' empty tiles
     vox::DecodeArgs d{};
@@ -411,7 +433,7 @@ int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const
       const int sp = hip_status(vox::launch_prefill(a, max_seqlen_q, s), "prefill_attn launch");
       if (sp != VOX_OK) return sp;
     }
-    return launch_decode_slices(d, batch, num_kv_heads, workspace, s);
+    return launch_decode_slices(d, batch, num_kv_heads, plan, workspace, s);
   }
   return hip_status(vox::launch_prefill(a, max_seqlen_q, s), "prefill_attn launch");
 }

@@ -14,6 +14,11 @@
 //    Every workgroup streams the same number of bytes; it walks its range sequence by sequence. The step layout
 //    comes from a scan of context_lens inside the kernel, so the launch shape depends only on host-known sizes
 //    (graph capture). The block table is staged in LDS when it fits, so block lookups never wait on memory.
+//  * Plan records: the layout depends only on the lengths and block tables, which every layer of a decode step
+//    shares. A launch in record mode writes each workgroup's part of it (its range, the sequences it touches, the
+//    block id of every tile it walks) into a 4 KiB record of the workspace; a later launch in reuse mode loads its
+//    record (one 16-byte load per thread) instead of staging the lengths and the table and scanning them, so its
+//    first tile loads go out one round trip after it starts.
 //  * A workgroup (4 waves) computes all query heads (<= 16) of a sequence at once. A cache slot row [HK][D] is
 //    contiguous (HK * 256 bytes), so the score GEMM contracts over the whole row c = (kv head, d) with a
 //    block-diagonal query operand B[c, h] = q[h, d] if c's kv head is h's group else 0: the 16 MFMA columns are 16
@@ -28,7 +33,8 @@
 //    directly; a sequence cut by range boundaries leaves one fp32 partial (O, m, l) per workgroup that touched it,
 //    at slot b + g (unique: the (sequence, workgroup) pairs form a monotone staircase), and decode_merge_kernel, next
 //    on the stream, combines them. (Merging in the split kernel itself, by the last workgroup to arrive, was measured
-//    slower: each workgroup then waits on a write-through and an atomic round trip.)
+//    slower: the arrival atomic and the device-coherent reads of the other pieces, issued after the slowest
+//    workgroup's last tile, cost more than this launch's gap and two round trips.)
 #include "vox_common.h"
 #include "vox_kernels.h"
 
@@ -59,6 +65,14 @@ constexpr int kMergeBatch = VOX_MERGE_BATCH;  // partials whose loads the merge 
 __device__ __forceinline__ f32x4 mfma_16x16x16(s16x4 a, s16x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
 }
+
+// Plan record of one workgroup (int32 offsets). The window holds up to 64 consecutive sequences from wb on: their
+// first and end steps, context, q / output row and new-token slot; then the block id of every tile of the range.
+constexpr int kRecValid = 0, kRecR = 1, kRecR1 = 2, kRecS = 3, kRecG = 4, kRecWb = 5, kRecBatch = 6, kRecGrid = 7;
+constexpr int kRecWin = 16;                       // [kRecWin + 64 a + k]: a = 0 st, 1 en, 2 ctx, 3 row, 4 snew
+constexpr int kRecTileOff = kRecWin + 5 * kWave;  // block id of range tile r + i
+constexpr int kRecTiles = kPlanRecInts - kRecTileOff;
+static_assert(kPlanRecInts == 4 * kThreads, "one 16-byte load per thread loads a record");
 
 template <int HK>
 struct Tile {
@@ -151,7 +165,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   __shared__ int s_start[kMaxSeqPerLaunch + 1];  // first step per sequence; s_start[batch] = total steps
   __shared__ int s_wtot[kWaves];
   __shared__ int s_wmax[kWaves];  // most steps of one sequence, per wave
-  __shared__ int s_bt[kBtLds];  // the block table, when it fits: no block-id round trips at segment starts
+  // the block table, when it fits (no block-id round trips at segment starts); in reuse mode the plan record
+  constexpr int kBtInts = BTL ? (kBtLds > kPlanRecInts ? kBtLds : kPlanRecInts) : kPlanRecInts;
+  __shared__ __attribute__((aligned(16))) int s_bt[kBtInts];
 
   const int g = blockIdx.x;
   const int tid = threadIdx.x;
@@ -166,12 +182,41 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   // lane / PPR, dims (lane % PPR) * 8 + [0, 8)
   const uint32_t koff = (uint32_t)(r16 * TT::ROW + jq * 8) * 2u;
   const uint32_t voff = (uint32_t)((lane / TT::PPR) * TT::ROW + (lane % TT::PPR) * 8) * 2u;
-
-  // ---- block table into LDS and the step layout (a block-wide prefix sum over ceil(context / 16)). The lengths of
-  // the first kThreads sequences and every table entry a thread stages are loaded before any of them is waited for:
-  // one round trip (a load-then-store loop waits for each load in turn, one round trip per kThreads entries).
   const int mb = p.max_blocks;
   const bool varlen = p.cu_q != nullptr;
+  const bool store = p.slot_mapping != nullptr;
+
+  // ---- the layout: from this workgroup's plan record (reuse mode), or from a block-wide scan
+  int S = 0, G = 1, r = 0, r1 = 0, wb = 0;
+  bool use_rec = false;
+  // the window: lane k holds sequence wb + k (its steps [w_st, w_en), context, row, new-token slot)
+  int w_st = 0, w_en = 0, w_ctx = 0, w_row = 0, w_snew = -1;
+  if (p.plan_mode == kPlanReuse) {
+    const u32x4 v = ld_g16(p.plan + (int64_t)g * kPlanRecInts + tid * 4);
+    *reinterpret_cast<u32x4*>(&s_bt[tid * 4]) = v;
+    __syncthreads();
+    r = s_bt[kRecR];
+    r1 = s_bt[kRecR1];
+    S = s_bt[kRecS];
+    G = s_bt[kRecG];
+    wb = s_bt[kRecWb];
+    // a record of this launch shape whose range fits it (the caller vouches for the rest: same lengths and tables)
+    use_rec = s_bt[kRecValid] == 1 && s_bt[kRecBatch] == p.batch && s_bt[kRecGrid] == (int)gridDim.x && G >= 1 &&
+              G <= (int)gridDim.x && 0 <= r && r <= r1 && r1 <= S && r1 - r <= kRecTiles &&
+              (r == r1 || (0 <= wb && wb < p.batch));
+    if (use_rec) {
+      w_st = s_bt[kRecWin + lane];
+      w_en = s_bt[kRecWin + kWave + lane];
+      w_ctx = s_bt[kRecWin + 2 * kWave + lane];
+      w_row = s_bt[kRecWin + 3 * kWave + lane];
+      w_snew = s_bt[kRecWin + 4 * kWave + lane];
+    } else {
+      __syncthreads();  // every wave has read the record's flags before the table staging below overwrites them
+      S = r = r1 = wb = 0;
+      G = 1;
+    }
+  }
+
   // sequence bb's context and row: context_lens[bb] and bb, or in varlen mode its key count when it has one query
   auto seq_of = [&](int bb, int& row) -> int {
     if (!varlen) {
@@ -182,95 +227,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
     row = q0;
     return q1 - q0 == 1 ? k1 - k0 : 0;
   };
-  // the first kThreads sequences' lengths and slots: loaded here, used after the table loads below are issued
-  int l0 = 0, l1 = 0, l2 = 0, l3 = 0, slot_first = -1;
-  if (tid < p.batch) {
-    if (varlen) {
-      l0 = p.cu_q[tid];
-      l1 = p.cu_q[tid + 1];
-      l2 = p.cu_k[tid];
-      l3 = p.cu_k[tid + 1];
-    } else {
-      l2 = p.context_lens[tid];
-    }
-    if (p.slot_mapping) slot_first = p.slot_mapping[tid];
-  }
-  if constexpr (BTL) {
-    constexpr int kPer = (kBtLds + kThreads - 1) / kThreads;  // entries per thread at most
-    const int nbt = p.batch * mb;
-    // entry i = tid + j kThreads sits at row i / mb, column i % mb; one step of kThreads entries moves the row by
-    // kThreads / mb and the column by kThreads % mb (with one carry at most)
-    const int dq = kThreads / mb, dr = kThreads % mb;
-    int row = tid / mb, col = tid % mb;
-    int vals[kPer];
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      vals[j] = tid + j * kThreads < nbt ? p.block_tables[(int64_t)row * p.bt_stride + col] : 0;
-      row += dq;
-      col += dr;
-      if (col >= mb) {
-        col -= mb;
-        ++row;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < kPer; ++j)
-      if (tid + j * kThreads < nbt) s_bt[tid + j * kThreads] = vals[j];
-  }
-  const int row_first = varlen ? l0 : tid;
-  const int ctx_first = !varlen ? l2 : (l1 - l0 == 1 ? l3 - l2 : 0);
-  int run = 0;
-  int nmax = 0;  // most steps of one sequence
-  for (int base = 0; base < p.batch; base += kThreads) {
-    const int bb = base + tid;
-    int row = row_first;
-    const int raw = base == 0 ? ctx_first : (bb < p.batch ? seq_of(bb, row) : 0);
-    const int ctx = bb < p.batch ? max(0, min(raw, max_ctx)) : 0;
-    const int n = (ctx + kTile - 1) / kTile;
-    const int incl = wave_incl_scan(n, lane);
-    int wmax = n;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) wmax = max(wmax, __shfl_xor(wmax, o, kWave));
-    if (lane == kWave - 1) {
-      s_wtot[w] = incl;
-      s_wmax[w] = wmax;
-    }
-    __syncthreads();
-    int before = 0, total = 0;
-#pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) {
-      before += ww < w ? s_wtot[ww] : 0;
-      total += s_wtot[ww];
-      nmax = max(nmax, s_wmax[ww]);
-    }
-    if (bb < p.batch) {
-      s_ctx[bb] = ctx;
-      if (p.slot_mapping) s_snew[bb] = base == 0 ? slot_first : p.slot_mapping[bb];
-      s_row[bb] = row;
-      s_start[bb] = run + before + incl - n;
-    }
-    run += total;
-    __syncthreads();
-  }
-  if (tid == 0) s_start[p.batch] = run;
-  __syncthreads();
-  const int S = uniform(run);
-  const int G = active_workgroups(gridDim.x, S, uniform(nmax));
-  if (g == 0) {  // the layout decode_merge_kernel reads, then the active workgroup count
-    for (int i = tid; i <= p.batch; i += kThreads) p.steps[i] = s_start[i];
-    if (tid == 0) p.steps[p.batch + 1] = G;
-  }
-
-  // this workgroup's range [r, r1)
-  if (g >= G) return;  // workgroup-uniform; WG 0 (always active) published the layout
-  const int r1 = (int)muldiv(g + 1, S, 0, G);
-  const int r = (int)muldiv(g, S, 0, G);
-
-  // Sequence lookups are lane-parallel (a ballot over LDS values the lanes read together) rather than walks of
-  // dependent LDS reads: at config 4 a binary search for the range's first sequence and serial walks to each wave's
-  // first tile took 2.8 us between the layout and the first tile loads, with HBM idle (a call: 41.6 -> 40.7 us).
   // The sequence holding range position x < S: the last b with s_start[b] <= x (an empty sequence shares its start
   // with the next one, so the last such b is not empty); a search over chunks of 64 sequences, then inside the chunk.
+  // (Lane-parallel ballots over LDS values rather than walks of dependent LDS reads: a binary search and serial walks
+  // had taken 2.8 us between the layout and the first tile loads at config 4.)
   auto seq_at = [&](int x) -> int {
     const int nch = (p.batch + kWave - 1) / kWave;  // <= 8 at kMaxSeqPerLaunch
     const int c0 = lane < nch ? s_start[lane * kWave] : INT32_MAX;
@@ -281,10 +241,128 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
     const uint64_t m1 = __builtin_amdgcn_ballot_w64(c1 <= x);
     return ch * kWave + 63 - __builtin_clzll(m1);
   };
-  // A round's window: lane k holds sequence wb + k (its steps [w_st, w_en), context, row, new-token slot), read in
-  // one LDS round trip; per-sequence values then come from the lane registers (v_readlane with a uniform index).
-  int w_st = 0, w_en = 0, w_ctx = 0, w_row = 0, w_snew = -1;
+  auto load_window = [&]() {  // from the LDS layout, one round trip
+    const int sq = wb + lane;
+    const bool in = sq < p.batch;
+    w_st = in ? s_start[sq] : S;
+    w_en = in ? s_start[sq + 1] : S;
+    w_ctx = in ? s_ctx[sq] : 0;
+    w_row = in ? s_row[sq] : 0;
+    w_snew = in && store ? s_snew[sq] : -1;
+  };
   auto lane_val = [&](int v, int k) { return __builtin_amdgcn_readlane(v, k); };
+
+  bool rec_write = false;  // record mode: this workgroup's record is valid and its tile block ids are written
+  int32_t* rec = p.plan + (int64_t)g * kPlanRecInts;
+  if (!use_rec) {
+    // ---- block table into LDS and the step layout (a block-wide prefix sum over ceil(context / 16)). The lengths
+    // of the first kThreads sequences and every table entry a thread stages are loaded before any of them is waited
+    // for: one round trip (a load-then-store loop waits for each load in turn, one round trip per kThreads entries).
+    int l0 = 0, l1 = 0, l2 = 0, l3 = 0, slot_first = -1;
+    if (tid < p.batch) {
+      if (varlen) {
+        l0 = p.cu_q[tid];
+        l1 = p.cu_q[tid + 1];
+        l2 = p.cu_k[tid];
+        l3 = p.cu_k[tid + 1];
+      } else {
+        l2 = p.context_lens[tid];
+      }
+      if (store) slot_first = p.slot_mapping[tid];
+    }
+    if constexpr (BTL) {
+      constexpr int kPer = (kBtLds + kThreads - 1) / kThreads;  // entries per thread at most
+      const int nbt = p.batch * mb;
+      // entry i = tid + j kThreads sits at row i / mb, column i % mb; one step of kThreads entries moves the row by
+      // kThreads / mb and the column by kThreads % mb (with one carry at most)
+      const int dq = kThreads / mb, dr = kThreads % mb;
+      int row = tid / mb, col = tid % mb;
+      int vals[kPer];
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        vals[j] = tid + j * kThreads < nbt ? p.block_tables[(int64_t)row * p.bt_stride + col] : 0;
+        row += dq;
+        col += dr;
+        if (col >= mb) {
+          col -= mb;
+          ++row;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kPer; ++j)
+        if (tid + j * kThreads < nbt) s_bt[tid + j * kThreads] = vals[j];
+    }
+    const int row_first = varlen ? l0 : tid;
+    const int ctx_first = !varlen ? l2 : (l1 - l0 == 1 ? l3 - l2 : 0);
+    int run = 0;
+    int nmax = 0;  // most steps of one sequence
+    for (int base = 0; base < p.batch; base += kThreads) {
+      const int bb = base + tid;
+      int row = row_first;
+      const int raw = base == 0 ? ctx_first : (bb < p.batch ? seq_of(bb, row) : 0);
+      const int ctx = bb < p.batch ? max(0, min(raw, max_ctx)) : 0;
+      const int n = (ctx + kTile - 1) / kTile;
+      const int incl = wave_incl_scan(n, lane);
+      int wmax = n;
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) wmax = max(wmax, __shfl_xor(wmax, o, kWave));
+      if (lane == kWave - 1) {
+        s_wtot[w] = incl;
+        s_wmax[w] = wmax;
+      }
+      __syncthreads();
+      int before = 0, total = 0;
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ++ww) {
+        before += ww < w ? s_wtot[ww] : 0;
+        total += s_wtot[ww];
+        nmax = max(nmax, s_wmax[ww]);
+      }
+      if (bb < p.batch) {
+        s_ctx[bb] = ctx;
+        if (store) s_snew[bb] = base == 0 ? slot_first : p.slot_mapping[bb];
+        s_row[bb] = row;
+        s_start[bb] = run + before + incl - n;
+      }
+      run += total;
+      __syncthreads();
+    }
+    if (tid == 0) s_start[p.batch] = run;
+    __syncthreads();
+    S = uniform(run);
+    G = active_workgroups(gridDim.x, S, uniform(nmax));
+    if (g == 0) {  // the layout decode_merge_kernel reads, then the active workgroup count (a record keeps it)
+      for (int i = tid; i <= p.batch; i += kThreads) p.steps[i] = s_start[i];
+      if (tid == 0) p.steps[p.batch + 1] = G;
+    }
+    if (g < G) {
+      r1 = (int)muldiv(g + 1, S, 0, G);
+      r = (int)muldiv(g, S, 0, G);
+      wb = seq_at(r);
+      load_window();
+    }
+    if (p.plan_mode == kPlanRecord && w == 0) {
+      // the record covers the range when the window reaches past it and the range's tiles fit
+      const bool valid = g >= G || (lane_val(w_en, kWave - 1) >= r1 && r1 - r <= kRecTiles);
+      rec_write = valid && g < G;
+      rec[kRecWin + lane] = w_st;
+      rec[kRecWin + kWave + lane] = w_en;
+      rec[kRecWin + 2 * kWave + lane] = w_ctx;
+      rec[kRecWin + 3 * kWave + lane] = w_row;
+      rec[kRecWin + 4 * kWave + lane] = w_snew;
+      if (lane < 8) {
+        const int hdr[8] = {valid ? 1 : 0, r, r1, S, G, wb, p.batch, (int)gridDim.x};
+        int v = hdr[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) v = lane == i ? hdr[i] : v;
+        rec[lane] = v;
+      }
+    }
+    rec_write = __builtin_amdgcn_readfirstlane(p.plan_mode == kPlanRecord &&
+                                               (g < G && lane_val(w_en, kWave - 1) >= r1 && r1 - r <= kRecTiles));
+  }
+
+  if (g >= G) return;  // workgroup-uniform; WG 0 (always active) published the layout
 
   const int hg = h < H ? h / p.group : -1;
   uint16_t* vt = s_vt + w * kTile * VROW;
@@ -294,14 +372,17 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   constexpr int kLOff = kMOff + kMaxHeads;
   const float c = p.scale_log2;
 
-  int wb = 0;       // the round window's first sequence
   uint64_t segs = 0;  // the round's segments: window lanes of the non-empty sequences it covers
   // block id of range tile t of the sequence at window lane k
   auto block_of = [&](int k, int t) -> int64_t {
+    if (use_rec) return uniform(s_bt[kRecTileOff + (t - r)]);
     const int col = (t - lane_val(w_st, k)) * kTile / p.block_size;
     const int bs = wb + k;
-    if constexpr (BTL) return uniform(s_bt[bs * mb + col]);
-    else return p.block_tables[(int64_t)bs * p.bt_stride + col];
+    int blk;
+    if constexpr (BTL) blk = uniform(s_bt[bs * mb + col]);
+    else blk = p.block_tables[(int64_t)bs * p.bt_stride + col];
+    if (rec_write && lane == 0) rec[kRecTileOff + (t - r)] = blk;
+    return blk;
   };
   // the round's next segment after window lane k
   auto next_seg = [&](int k) { return __builtin_ctzll(k >= 63 ? 0ull : (segs >> (k + 1)) << (k + 1)); };
@@ -309,7 +390,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
     T.ok = blk >= 0 && blk < p.num_blocks;
     const int tok = (t - lane_val(w_st, k)) * kTile;
     const int64_t slot0 = (T.ok ? blk : 0) * p.block_size + (tok % p.block_size);
-    if (!p.slot_mapping) {
+    if (!store) {
       load_tile<HK>(T, p, slot0, koff, voff);
       return;
     }
@@ -330,27 +411,21 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
 
   int rr = r;   // round start (range position)
   while (rr < r1) {
-    // the round: up to kRoundSegs non-empty sequences from the one holding rr, those starting before r1, within
-    // one 64-sequence window (a round over a window with fewer segments ends at the window's last one)
-    wb = seq_at(rr);
-    {
-      const int sq = wb + lane;
-      const bool in = sq < p.batch;
-      w_st = in ? s_start[sq] : S;
-      w_en = in ? s_start[sq + 1] : S;
-      w_ctx = in ? s_ctx[sq] : 0;
-      w_row = in ? s_row[sq] : 0;
-      w_snew = in && p.slot_mapping ? s_snew[sq] : -1;
+    // the round: up to kRoundSegs non-empty sequences of the window that end after rr and start before r1 (a round
+    // over a window with fewer segments ends at the window's last one; the next round moves the window on)
+    if (!use_rec && lane_val(w_en, kWave - 1) <= rr) {
+      wb = seq_at(rr);
+      load_window();
     }
-    const uint64_t cand = __builtin_amdgcn_ballot_w64(w_en > w_st && w_st < r1);  // lane 0 at least
+    const uint64_t cand = __builtin_amdgcn_ballot_w64(w_en > w_st && w_en > rr && w_st < r1);
     const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(cand >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)cand, 0));
     segs = __builtin_amdgcn_ballot_w64(((cand >> lane) & 1ull) && below < kRoundSegs);
     const int nseg = __builtin_popcountll(segs);
-    const int re = min(r1, lane_val(w_en, 63 - __builtin_clzll(segs)));
+    const int k_first = __builtin_ctzll(segs), k_last = 63 - __builtin_clzll(segs);
+    const int re = min(r1, lane_val(w_en, k_last));
     const int R = re - rr;
     auto share_lo = [&](int ww) { return rr + (int)(((int64_t)R * ww) / kWaves); };
     const int t_lo = share_lo(w), t_hi = share_lo(w + 1);
-
     if (t_lo < t_hi) {
       // this wave's first tile: window lane kcur, round segment kc
       const uint64_t hold = __builtin_amdgcn_ballot_w64(((segs >> lane) & 1ull) && w_st <= t_lo && t_lo < w_en);

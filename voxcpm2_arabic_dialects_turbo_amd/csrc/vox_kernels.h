@@ -12,6 +12,11 @@ constexpr int kPartialFloats = 16 * 128 + 16 + 16;
 constexpr int kMaxSeqPerLaunch = 512;
 // Block-table entries (batch x max_blocks) a decode launch keeps in LDS; wider tables are read from global memory.
 constexpr int kBtLds = 3584;
+// Decode plan records (int32 per workgroup) and the plan modes of a decode launch: none (the layout from a scan in
+// every workgroup), record (the same, and each workgroup writes its record), reuse (each workgroup loads the record
+// an earlier launch over the same lengths, tables and slots wrote; a record that does not fit falls back to the scan)
+constexpr int kPlanRecInts = 1024;
+constexpr int kPlanNone = 0, kPlanRecord = 1, kPlanReuse = 2;
 
 struct DecodeArgs {
   const uint16_t* q;          // bf16 [B, H, 128]; sequence rows q_row_stride apart, heads 128 apart
@@ -30,7 +35,9 @@ struct DecodeArgs {
   float scale_log2;           // softmax_scale * log2(e)
   int grid;                   // workgroups of the split kernel (persistent, balanced ranges)
   float* partials;            // [B + grid, kPartialFloats]
-  int32_t* steps;             // [B + 2]: first 64-token step of every sequence, the total, the active workgroups
+  int32_t* steps;             // [B + 2]: first step of every sequence, the total, the active workgroups
+  int32_t* plan;              // [grid, kPlanRecInts]: one record per workgroup
+  int plan_mode;              // kPlanNone, kPlanRecord (write the records and the steps), kPlanReuse (read them)
   uint16_t* out;              // bf16 [B, H, 128]: sequence rows out_row_stride apart, heads 128 apart
   int64_t out_row_stride;
   // Varlen mode (cu_q != nullptr; context_lens unused): the one-query rows of a varlen call. Sequence b is handled

@@ -19,11 +19,14 @@ module can be captured into HIP graphs exactly where the reference captures its 
 
 from __future__ import annotations
 
+import itertools
+
 import torch
 from torch import nn
 
 from .context import get_context
-from .ops import decode_attention, flash_attn_func, flash_attn_varlen_func, flash_attn_with_kvcache, store_kvcache
+from .ops import (decode_attention, flash_attn_func, flash_attn_varlen_func, flash_attn_with_kvcache, planning,
+                  store_kvcache)
 
 __all__ = ["Attention", "store_kvcache"]
 
@@ -42,6 +45,25 @@ def _store_rides_in_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sl
                 or t.stride(0) < t.shape[1] * t.shape[2]:
             return False
     return True
+
+
+_PLAN_SERIAL = itertools.count(1)
+
+
+def _plan_key(context) -> tuple:
+    """The decode-plan key of a forward context: one serial per context object (a new set_context is a new step) and
+    the tensors the layout is read from, so every layer of a step shares one plan and a context whose tensors are
+    swapped (last_rows) records its own."""
+    serial = context.__dict__.get("_vox_plan_serial")
+    if serial is None:
+        serial = next(_PLAN_SERIAL)
+        context._vox_plan_serial = serial
+
+    def ident(t):
+        return None if t is None else (t.data_ptr(), tuple(t.shape), tuple(t.stride()))
+
+    return (serial, ident(context.context_lens), ident(context.block_tables), ident(context.slot_mapping),
+            ident(context.cu_seqlens_q), ident(context.cu_seqlens_k))
 
 
 class Attention(nn.Module):
@@ -71,24 +93,27 @@ class Attention(nn.Module):
                 # decode step: the store rides in the decode call (one row per sequence, each writing the slot of
                 # its own newest token)
                 return decode_attention(q, k_cache, v_cache, context.context_lens, context.block_tables, self.scale,
-                                        key=k, value=v, slot_mapping=context.slot_mapping).unsqueeze(1)
+                                        key=k, value=v, slot_mapping=context.slot_mapping,
+                                        plan=_plan_key(context)).unsqueeze(1)
             if cached:
                 store_kvcache(k, v, k_cache, v_cache, context.slot_mapping)
             if context.is_prefill:
                 if context.block_tables is not None:  # prefix cache: keys through the block tables
                     k, v = k_cache, v_cache
-                o = flash_attn_varlen_func(
-                    q,
-                    k,
-                    v,
-                    max_seqlen_q=context.max_seqlen_q,
-                    cu_seqlens_q=context.cu_seqlens_q,
-                    max_seqlen_k=context.max_seqlen_k,
-                    cu_seqlens_k=context.cu_seqlens_k,
-                    softmax_scale=self.scale,
-                    causal=True,
-                    block_table=context.block_tables,
-                )
+                # (a mixed step's one-query rows run on the decode kernel: their layout is planned per context)
+                with planning(_plan_key(context) if context.block_tables is not None else None):
+                    o = flash_attn_varlen_func(
+                        q,
+                        k,
+                        v,
+                        max_seqlen_q=context.max_seqlen_q,
+                        cu_seqlens_q=context.cu_seqlens_q,
+                        max_seqlen_k=context.max_seqlen_k,
+                        cu_seqlens_k=context.cu_seqlens_k,
+                        softmax_scale=self.scale,
+                        causal=True,
+                        block_table=context.block_tables,
+                    )
             else:  # decode
                 o = flash_attn_with_kvcache(
                     q.unsqueeze(1),

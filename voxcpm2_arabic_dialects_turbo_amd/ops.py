@@ -12,6 +12,8 @@ int32 index tensors. Decode takes up to 16 query heads over 1 or 2 KV heads.
 
 from __future__ import annotations
 
+import threading
+
 import torch
 
 from . import _lib
@@ -74,13 +76,88 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
 
 
 # --------------------------------------------------------------------------------------------------------------------
+# Decode workspace and plans
+#
+# A decode call that reuses a plan reads the plan records and the step layout an earlier call left in the workspace, so
+# the workspace is made once per device and workgroup count (room for a full 512-sequence launch; its layout depends on
+# the workgroup count) and kept for the life of the process, since a captured graph holds its address. Decode calls on
+# one device therefore share it and must not overlap (the engine runs them on one stream).
+#
+# Plans: the layout of a decode step (which tiles each workgroup walks) is the same for every layer of the step.
+# Callers that know when a step's layout repeats pass a `plan` key (Attention.forward: the forward context, see
+# layers.py); the first call with a new key records the layout in the workspace, later calls with the same key reuse
+# it. The key also carries the graph capture in progress, so a capture always records its own plan in its first call.
+
+_WS_LOCK = threading.Lock()
+_WORKSPACE: dict[tuple[int, int], torch.Tensor] = {}
+_PLANNED: dict[int, object] = {}
+
+
+def _device_index(dev: torch.device) -> int:
+    return dev.index if dev.index is not None else torch.cuda.current_device()
+
+
+def decode_workspace(dev: torch.device) -> torch.Tensor:
+    """The persistent decode workspace (uint8) of the device at the current workgroup count, made zero-filled on
+    first use."""
+    lib = _lib.load()
+    key = (_device_index(dev), int(lib.vox_decode_workgroups()))
+    with _WS_LOCK:
+        ws = _WORKSPACE.get(key)
+        if ws is None:
+            ws = torch.zeros(max(int(lib.vox_decode_workspace_bytes(512)), 256), dtype=torch.uint8, device=dev)
+            _WORKSPACE[key] = ws
+        return ws
+
+
+def _plan_mode(dev: torch.device, plan, *shape) -> int:
+    """The plan mode of a call with key `plan` (None: no plan) over launch shape `shape` on `dev`'s workspace."""
+    if plan is None:
+        return _lib.PLAN_NONE
+    lib = _lib.load()
+    key = (plan, shape, int(lib.vox_decode_workgroups()), _lib.capture_id(_lib.stream_handle(dev)))
+    idx = _device_index(dev)
+    with _WS_LOCK:
+        if _PLANNED.get(idx) == key:
+            return _lib.PLAN_REUSE
+        _PLANNED[idx] = key
+        return _lib.PLAN_RECORD
+
+
+_SCOPE = threading.local()
+
+
+class planning:
+    """Within the block, varlen calls made without a `plan` key use `key` (how Attention.forward plans the decode rows
+    of a mixed step through flash_attn_varlen_func, whose signature is flash-attn's)."""
+
+    def __init__(self, key):
+        self.key = key
+
+    def __enter__(self):
+        self.prev = getattr(_SCOPE, "key", None)
+        _SCOPE.key = self.key
+        return self
+
+    def __exit__(self, *exc):
+        _SCOPE.key = self.prev
+        return False
+
+
+def forget_plans() -> None:
+    """Drops every recorded plan key (the next planned call on each device records again)."""
+    with _WS_LOCK:
+        _PLANNED.clear()
+
+
+# --------------------------------------------------------------------------------------------------------------------
 # Decode
 
 
 def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, context_lens: torch.Tensor,
                      block_tables: torch.Tensor, softmax_scale: float, out: torch.Tensor | None = None,
                      key: torch.Tensor | None = None, value: torch.Tensor | None = None,
-                     slot_mapping: torch.Tensor | None = None) -> torch.Tensor:
+                     slot_mapping: torch.Tensor | None = None, plan=None) -> torch.Tensor:
     """One query token per sequence: q [B, H, 128] (sequence rows may be strided) over the paged cache
     [num_blocks, block_size, HK, 128] through block_tables int32 [B, max_blocks]; context_lens int32 [B].
     Returns o [B, H, 128] bf16 (contiguous). Rows with context_lens == 0 get zeros.
@@ -88,7 +165,11 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     With key / value ([B, HK, 128], rows may be strided) and slot_mapping ([B]), the decode step's KV store happens
     in the same call: the result (and the caches afterwards) are those of store_kvcache(key, value, k_cache,
     v_cache, slot_mapping) followed by this attention, as long as no sequence's slot lies inside another
-    sequence's context (the engine's decode steps: each sequence writes its own last block)."""
+    sequence's context (the engine's decode steps: each sequence writes its own last block).
+
+    ``plan``: a hashable key that stays the same exactly as long as context_lens, block_tables and slot_mapping hold
+    the same values (Attention.forward passes one per forward context): the first call with a key records the
+    decode layout, later ones reuse it (see the plan notes above)."""
     B, H, D = q.shape
     dev = _check_cuda(q, k_cache, v_cache, context_lens, block_tables)
     if q.dtype != torch.bfloat16 or k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
@@ -117,12 +198,12 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     lens = _as_i32(context_lens.reshape(-1), "context_lens")
     max_blocks = bt.shape[1]
     lib = _lib.load()
-    ws_bytes = lib.vox_decode_workspace_bytes(B)
-    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    ws = decode_workspace(dev)
+    mode = _plan_mode(dev, plan, "decode", key is not None, B, max_blocks, bt.stride(0), H, HK, block_size)
     if key is None:
         _lib.check(lib.vox_decode_attn(q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), num_blocks,
                                        block_size, bt.data_ptr(), bt.stride(0), max_blocks, lens.data_ptr(), B, H, HK,
-                                       D, float(softmax_scale), ws.data_ptr(), ws.numel(), out.data_ptr(),
+                                       D, float(softmax_scale), mode, ws.data_ptr(), ws.numel(), out.data_ptr(),
                                        _lib.stream_handle(dev)),
                    "decode_attn")
         return out
@@ -139,7 +220,7 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     _lib.check(lib.vox_decode_attn_store(q.data_ptr(), q.stride(0), key.data_ptr(), value.data_ptr(), key.stride(0),
                                          value.stride(0), slots.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
                                          num_blocks, block_size, bt.data_ptr(), bt.stride(0), max_blocks,
-                                         lens.data_ptr(), B, H, HK, D, float(softmax_scale), ws.data_ptr(),
+                                         lens.data_ptr(), B, H, HK, D, float(softmax_scale), mode, ws.data_ptr(),
                                          ws.numel(), out.data_ptr(), _lib.stream_handle(dev)),
                "decode_attn_store")
     return out
@@ -154,13 +235,15 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor | None, v: torch.Tensor | 
                      softmax_scale: float, causal: bool, block_table: torch.Tensor | None = None,
                      k_cache: torch.Tensor | None = None, v_cache: torch.Tensor | None = None,
                      batch: int | None = None, uniform_seqlen_q: int = 0, uniform_seqlen_k: int = 0,
-                     out: torch.Tensor | None = None, quant: bool = False, inv_smooth: torch.Tensor | None = None):
+                     out: torch.Tensor | None = None, quant: bool = False, inv_smooth: torch.Tensor | None = None,
+                     plan=None):
     """The varlen prefill kernel. q [T, H, 128] (token rows may be strided). K/V from packed rows k / v
     [Tk, HK, 128] or, with block_table, from k_cache / v_cache [num_blocks, block_size, HK, 128]. Sequences from
     cu_seqlens_q / cu_seqlens_k (int32 [B + 1]) or, when both are None, `batch` sequences of uniform lengths.
     Returns o [T, H, 128] bf16; with ``quant`` (HK <= 2), (int8 o [T, H * 128], fp32 scale [T]): per token
     o * inv_smooth (fp32 [H * 128], optional) over all heads quantized to rint(o / scale), scale = max(amax, 1e-6) / 127
-    (reference: the QUANT epilogues of kernels/prefill_attn.py:84-92, kernels/short_attn.py:55-64, 137-146)."""
+    (reference: the QUANT epilogues of kernels/prefill_attn.py:84-92, kernels/short_attn.py:55-64, 137-146).
+    ``plan``: as decode_attention's, for the one-query rows a paged varlen call runs on the decode kernel."""
     T, H, D = q.shape
     dev = _check_cuda(q)
     if q.dtype != torch.bfloat16:
@@ -241,14 +324,17 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor | None, v: torch.Tensor | 
     # workspace. Passed when every row has one query, or when the (q tile, sequence) grid would be mostly empty
     # (T rows against B sequences of up to max_seqlen_q), which is what a few prefills beside many decode rows look
     # like; a dense prefill keeps the plain grid (a 44 x 46 paged step: 12.8 us there, 20.5 us persistent).
-    ws = None
+    ws, mode = None, _lib.PLAN_NONE
     if block_table is not None and cu_q is not None and (max_seqlen_q == 1 or 4 * T <= B * max_seqlen_q):
-        ws = torch.empty(max(lib.vox_prefill_workspace_bytes(B), 16), dtype=torch.uint8, device=dev)
+        ws = decode_workspace(dev)
+        if plan is None:
+            plan = getattr(_SCOPE, "key", None)
+        mode = _plan_mode(dev, plan, "varlen", B, int(block_table.shape[1]), H, HK, int(k_cache.shape[1]))
     _lib.check(lib.vox_prefill_attn(q.data_ptr(), q.stride(0), *args,
                                     None if cu_q is None else cu_q.data_ptr(),
                                     None if cu_k is None else cu_k.data_ptr(), B, int(max_seqlen_q),
                                     int(uniform_seqlen_q), int(uniform_seqlen_k), H, HK, D, float(softmax_scale),
-                                    1 if causal else 0, out.data_ptr(), out.stride(0),
+                                    1 if causal else 0, out.data_ptr(), out.stride(0), mode,
                                     None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
                                     _lib.stream_handle(dev)),
                "prefill_attn")
