@@ -168,6 +168,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   // the block table, when it fits (no block-id round trips at segment starts); in reuse mode the plan record
   constexpr int kBtInts = BTL ? (kBtLds > kPlanRecInts ? kBtLds : kPlanRecInts) : kPlanRecInts;
   __shared__ __attribute__((aligned(16))) int s_bt[kBtInts];
+  __shared__ int s_rtiles[kRecTiles];  // record mode: the block id of every tile of the range, for the record
 
   const int g = blockIdx.x;
   const int tid = threadIdx.x;
@@ -252,8 +253,22 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
   };
   auto lane_val = [&](int v, int k) { return __builtin_amdgcn_readlane(v, k); };
 
-  bool rec_write = false;  // record mode: this workgroup's record is valid and its tile block ids are written
+  bool rec_write = false;  // record mode: this workgroup's record is valid (its tile block ids are collected)
   int32_t* rec = p.plan + (int64_t)g * kPlanRecInts;
+  auto write_record = [&](bool valid) {  // header and window of the record, by one wave
+    rec[kRecWin + lane] = w_st;
+    rec[kRecWin + kWave + lane] = w_en;
+    rec[kRecWin + 2 * kWave + lane] = w_ctx;
+    rec[kRecWin + 3 * kWave + lane] = w_row;
+    rec[kRecWin + 4 * kWave + lane] = w_snew;
+    if (lane < 8) {
+      const int hdr[8] = {valid ? 1 : 0, r, r1, S, G, wb, p.batch, (int)gridDim.x};
+      int v = hdr[0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) v = lane == i ? hdr[i] : v;
+      rec[lane] = v;
+    }
+  };
   if (!use_rec) {
     // ---- block table into LDS and the step layout (a block-wide prefix sum over ceil(context / 16)). The lengths
     // of the first kThreads sequences and every table entry a thread stages are loaded before any of them is waited
@@ -341,25 +356,12 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
       wb = seq_at(r);
       load_window();
     }
-    if (p.plan_mode == kPlanRecord && w == 0) {
-      // the record covers the range when the window reaches past it and the range's tiles fit
-      const bool valid = g >= G || (lane_val(w_en, kWave - 1) >= r1 && r1 - r <= kRecTiles);
-      rec_write = valid && g < G;
-      rec[kRecWin + lane] = w_st;
-      rec[kRecWin + kWave + lane] = w_en;
-      rec[kRecWin + 2 * kWave + lane] = w_ctx;
-      rec[kRecWin + 3 * kWave + lane] = w_row;
-      rec[kRecWin + 4 * kWave + lane] = w_snew;
-      if (lane < 8) {
-        const int hdr[8] = {valid ? 1 : 0, r, r1, S, G, wb, p.batch, (int)gridDim.x};
-        int v = hdr[0];
-#pragma unroll
-        for (int i = 1; i < 8; ++i) v = lane == i ? hdr[i] : v;
-        rec[lane] = v;
-      }
-    }
+    // record mode: the record covers the range when the window reaches past it and the range's tiles fit. An active
+    // workgroup collects its tiles' block ids in LDS and writes the record when its range is done: a global store
+    // among the tile loads made the compiler's waits for those loads wait for the store too (+2 us per call)
     rec_write = __builtin_amdgcn_readfirstlane(p.plan_mode == kPlanRecord &&
                                                (g < G && lane_val(w_en, kWave - 1) >= r1 && r1 - r <= kRecTiles));
+    if (p.plan_mode == kPlanRecord && g >= G && w == 0) write_record(true);  // (no range)
   }
 
   if (g >= G) return;  // workgroup-uniform; WG 0 (always active) published the layout
@@ -381,7 +383,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
     int blk;
     if constexpr (BTL) blk = uniform(s_bt[bs * mb + col]);
     else blk = p.block_tables[(int64_t)bs * p.bt_stride + col];
-    if (rec_write && lane == 0) rec[kRecTileOff + (t - r)] = blk;
+    if (rec_write && lane == 0) s_rtiles[t - r] = blk;
     return blk;
   };
   // the round's next segment after window lane k
@@ -632,6 +634,11 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs p) {
     }
     __syncthreads();  // the slots and V tiles are free for the next round
     rr = re;
+  }
+  if (p.plan_mode == kPlanRecord) {  // the record of this workgroup's range (tile ids collected behind the barrier)
+    if (w == 0) write_record(rec_write);
+    if (rec_write)
+      for (int i = tid; i < r1 - r; i += kThreads) rec[kRecTileOff + i] = s_rtiles[i];
   }
 }
 
