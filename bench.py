@@ -530,7 +530,43 @@ def bench_prefill(dev):
     tf2 = flops2 / (ms2 * 1e-3) / 1e12
     out["long_16x2048_supplementary"] = dict(launch_us=round(ms2 * 1e3, 1), tflops=round(tf2, 1),
                                              pct_mfma_peak=round(100 * tf2 / MFMA_BF16_PEAK_TFLOPS, 2))
+    del big, o2
+    out["chain_latency"] = bench_chain_latency(dev)
     return out
+
+
+def bench_chain_latency(dev, sets: int = 32):
+    """Launch time of one causal sequence of n tokens, for growing n: the sequence's heaviest work item (its last q
+    tile) walks ceil(n / 64) key tiles one after another, and the light items run beside it, so the launch time
+    against that count gives the fixed start and the cost per key tile of a chain (what bounds config 2). Inputs
+    rotate over `sets` copies per length."""
+    import torch
+
+    from voxcpm2_arabic_dialects_turbo_amd.ops import varlen_attention
+
+    rows, xs, ys = [], [], []
+    for n in (64, 128, 256, 512, 1024):
+        buf = torch.randn(sets, n, (H + 2 * HK) * D, generator=torch.Generator(device=dev).manual_seed(52),
+                          device=dev).to(torch.bfloat16)
+        cu1 = torch.tensor([0, n], dtype=torch.int32, device=dev)
+        o1 = torch.empty(n, H, D, dtype=torch.bfloat16, device=dev)
+
+        def run():
+            for s in range(sets):
+                q, k, v = buf[s].split([H * D, HK * D, HK * D], dim=-1)
+                varlen_attention(q.view(n, H, D), k.view(n, HK, D), v.view(n, HK, D), cu_seqlens_q=cu1,
+                                 cu_seqlens_k=cu1, max_seqlen_q=n, softmax_scale=SCALE, causal=True, out=o1)
+
+        us = _graph_ms(run, 20) / sets * 1e3
+        tiles = (n + 63) // 64
+        rows.append(dict(tokens=n, key_tiles_of_heaviest_item=tiles, launch_us=round(us, 2)))
+        xs.append(tiles)
+        ys.append(us)
+        del buf, o1
+    mx, my = sum(xs) / len(xs), sum(ys) / len(ys)
+    slope = sum((x - mx) * (y - my) for x, y in zip(xs, ys)) / sum((x - mx) ** 2 for x in xs)
+    return dict(what="one causal sequence per launch (16 q / 2 kv heads), launch time by length", runs=rows,
+                fit_us_per_key_tile=round(slope, 3), fit_start_us=round(my - slope * mx, 2))
 
 
 def bench_reference_shapes(dev):
