@@ -12,6 +12,7 @@ import torch
 from oracle import attention as ref
 from tests._util import BLOCK, D, H, HK, attn_close, paged_pool, randn, uniform_lens
 from tests.golden import make_golden
+from voxcpm2_arabic_dialects_turbo_amd import _lib
 from voxcpm2_arabic_dialects_turbo_amd.kernels.prefill_attn import paged_prefill_attention
 from voxcpm2_arabic_dialects_turbo_amd.kernels.short_attn import short_attention, short_causal_attention
 from voxcpm2_arabic_dialects_turbo_amd.ops import flash_attn_func, flash_attn_varlen_func, store_kvcache
@@ -493,23 +494,26 @@ def test_mixed_step_captured_in_a_hip_graph_replays_like_eager():
         assert torch.equal(other, eager2)
 
 
-def test_mixed_step_with_a_prefill_longer_than_the_rank_order_covers():
+@pytest.mark.parametrize("n,bs", [(4200, 32), (8500, BLOCK)])
+def test_mixed_step_with_a_prefill_longer_than_the_rank_order_covers(n, bs):
     """A mixed step (one-query rows on the decode kernels) whose prefill spans more than 1024 query tiles takes the
-    persistent prefill's sequence-by-sequence order: 16 query heads over 1 kv head (4 tokens per tile), a 4200-token
-    prefill beside ten decode rows; its first and last 100 query rows are checked against the oracle."""
+    persistent prefill's sequence-by-sequence order: 16 query heads over 1 kv head, a prefill of n tokens beside ten
+    decode rows; with 32-token blocks the persistent prefill launch (4 tokens per tile) then the decode launch, with
+    256-token blocks the mixed launch (8 tokens per tile). Its first and last 100 query rows are checked against the
+    oracle."""
     gen = torch.Generator().manual_seed(92)
     H1, HK1 = 16, 1
-    n = 4200
     dec = [300, 77, 1, 256, 257, 900, 5, 600, 1000, 2]
     nq, nk = [n] + [1] * len(dec), [n] + dec
-    pool = 17 + sum((x + BLOCK - 1) // BLOCK for x in dec) + 2
-    kc = randn(gen, pool, BLOCK, HK1, D)
-    vc = randn(gen, pool, BLOCK, HK1, D)
+    width = (n + bs - 1) // bs
+    pool = width + sum((x + bs - 1) // bs for x in dec) + 2
+    kc = randn(gen, pool, bs, HK1, D)
+    vc = randn(gen, pool, bs, HK1, D)
     perm = torch.randperm(pool, generator=gen).tolist()
-    tables = torch.full((len(nk), 17), -1, dtype=torch.int32)
+    tables = torch.full((len(nk), width), -1, dtype=torch.int32)
     at = 0
     for b, x in enumerate(nk):
-        nb = (x + BLOCK - 1) // BLOCK
+        nb = (x + bs - 1) // bs
         tables[b, :nb] = torch.tensor(perm[at:at + nb])
         at += nb
     q = randn(gen, sum(nq), H1, D)
@@ -522,3 +526,78 @@ def test_mixed_step_with_a_prefill_longer_than_the_rank_order_covers():
         attn_close(out[i0:i1], want, f"long prefill rows {i0}:{i1}")
     want = ref.varlen(q[n:].float(), _cu(nq[1:]), _cu(nk[1:]), k_cache=kc, v_cache=vc, block_tables=tables[1:])
     attn_close(out[n:], want, "decode rows beside the long prefill")
+
+
+def _mixed_case(gen, n_dec, dec_hi, pre_lens, hk, block_size=64):
+    """A mixed step: prefills pre_lens (with a cached prefix of up to 100 tokens) and n_dec one-query rows over
+    0..dec_hi keys, a paged pool of block_size-token blocks with hk kv heads."""
+    nq = list(pre_lens) + [1] * n_dec
+    nk = [n + int(torch.randint(0, 101, (1,), generator=gen)) for n in pre_lens] + \
+        torch.randint(0, dec_hi + 1, (n_dec,), generator=gen).tolist()
+    pool = sum((n + block_size - 1) // block_size for n in nk) + 5
+    kc, vc, tables = paged_pool(gen, nk, pool, block_size=block_size, hk=hk)
+    return nq, nk, kc, vc, tables
+
+
+@pytest.mark.parametrize("grid", [1, 8, 0])
+@pytest.mark.parametrize("h,hk", [(16, 2), (16, 1)])
+def test_mixed_launch_with_many_decode_rows_per_workgroup(grid, h, hk):
+    """The mixed launch (one-query rows on decode workgroups, each sharing a CU with a prefill workgroup, rounds of
+    three sequences with bf16 wave partials): 248 one-query rows over 0-40 keys and 8 prefills (256 sequences, the
+    launch's limit), over a decode grid of 1, 8 or one workgroup per CU, so that one workgroup's range holds from a
+    few to every row (one round to a hundred)."""
+    gen = torch.Generator().manual_seed(93 + grid + hk)
+    nq, nk, kc, vc, tables = _mixed_case(gen, 248, 40, uniform_lens(gen, 8, 2, 200), hk)
+    q = randn(gen, sum(nq), h, D)
+    lib = _lib.load()
+    lib.vox_set_decode_workgroups(grid)
+    try:
+        out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), _cu(nq).to(DEV), _cu(nk).to(DEV), max(nq),
+                                     max(nk), softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
+        torch.cuda.synchronize()
+    finally:
+        lib.vox_set_decode_workgroups(0)
+    want = ref.varlen(q.float(), _cu(nq), _cu(nk), k_cache=kc, v_cache=vc, block_tables=tables)
+    attn_close(out, want, f"mixed launch, decode grid {grid}, {h}/{hk} heads")
+    zero_rows = [sum(nq[:b]) for b in range(8, 256) if nk[b] == 0]
+    for r in zero_rows:
+        assert out[r].float().abs().max().item() == 0.0, "a one-query row without keys gives zeros"
+
+
+@pytest.mark.parametrize("n_seq", [256, 257])
+def test_mixed_step_at_and_past_the_mixed_launch_limit(n_seq):
+    """256 sequences run as one mixed launch, 257 as the persistent prefill launch then the decode launch: both
+    against the oracle (config-5 lengths: prefills of 300-600 tokens, decode rows over 128-1800 keys)."""
+    gen = torch.Generator().manual_seed(94 + n_seq)
+    pre = uniform_lens(gen, 6, 300, 600)
+    dec = uniform_lens(gen, n_seq - 6, 128, 1800)
+    nq, nk = pre + [1] * len(dec), pre + dec
+    pool = sum((n + BLOCK - 1) // BLOCK for n in nk) + 3
+    kc, vc, tables = paged_pool(gen, nk, pool)
+    q = randn(gen, sum(nq), H, D)
+    out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), _cu(nq).to(DEV), _cu(nk).to(DEV), max(nq),
+                                 max(nk), softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
+    want = ref.varlen(q.float(), _cu(nq), _cu(nk), k_cache=kc, v_cache=vc, block_tables=tables)
+    attn_close(out, want, f"{n_seq} sequences")
+
+
+def test_mixed_launch_plan_recorded_then_reused_equals_unplanned():
+    """The decode rows of a mixed launch plan like a decode step's layers: a call that records the layout and two
+    that reuse it (the 28 layers of a mixed step share their lengths and tables) equal the unplanned call bit for
+    bit."""
+    from voxcpm2_arabic_dialects_turbo_amd.ops import forget_plans, varlen_attention
+
+    gen = torch.Generator().manual_seed(95)
+    nq, nk, kc, vc, tables = _mixed_case(gen, 120, 1800, uniform_lens(gen, 6, 300, 600), HK, block_size=BLOCK)
+    q = randn(gen, sum(nq), H, D).to(DEV)
+    kw = dict(cu_seqlens_q=_cu(nq).to(DEV), cu_seqlens_k=_cu(nk).to(DEV), max_seqlen_q=max(nq), softmax_scale=SCALE,
+              causal=True, block_table=tables.to(DEV), k_cache=kc.to(DEV), v_cache=vc.to(DEV))
+    forget_plans()
+    plain = varlen_attention(q, None, None, **kw)
+    planned = [varlen_attention(q, None, None, plan=("mixed plan test", 1), **kw) for _ in range(3)]
+    torch.cuda.synchronize()
+    forget_plans()
+    for i, o in enumerate(planned):
+        assert torch.equal(o, plain), f"call {i} ({'record' if i == 0 else 'reuse'}) differs from the unplanned one"
+    want = ref.varlen(q.float().cpu(), _cu(nq), _cu(nk), k_cache=kc, v_cache=vc, block_tables=tables)
+    attn_close(plain, want, "mixed launch, planned")

@@ -108,15 +108,22 @@ namespace {
 // Launches the decode kernel over `batch` sequences in slices of kMaxSeqPerLaunch (each slice's step layout lives
 // in LDS), all sharing the workspace; `a` describes the whole batch. A call of several slices runs unplanned (the
 // workspace holds one plan).
+// a's split-KV scratch and plan records in the workspace, for launches of up to `slice` sequences
+vox::DecodeArgs with_workspace(const vox::DecodeArgs& a, int slice, int plan_mode, void* workspace) {
+  const DecodeWorkspace ws = decode_workspace(slice, a.grid);
+  vox::DecodeArgs d = a;
+  d.partials = (float*)((char*)workspace + ws.partials);
+  d.steps = (int32_t*)((char*)workspace + ws.steps);
+  d.plan = (int32_t*)((char*)workspace + ws.plan);
+  d.plan_mode = plan_mode;
+  return d;
+}
+
 int launch_decode_slices(const vox::DecodeArgs& a, int batch, int num_kv_heads, int plan, void* workspace,
                          hipStream_t stream) {
   const int slice_max = batch < vox::kMaxSeqPerLaunch ? batch : vox::kMaxSeqPerLaunch;
-  const DecodeWorkspace ws = decode_workspace(slice_max, a.grid);
-  vox::DecodeArgs base = a;
-  base.partials = (float*)((char*)workspace + ws.partials);
-  base.steps = (int32_t*)((char*)workspace + ws.steps);
-  base.plan = (int32_t*)((char*)workspace + ws.plan);
-  base.plan_mode = batch <= vox::kMaxSeqPerLaunch ? plan : vox::kPlanNone;
+  const vox::DecodeArgs base =
+      with_workspace(a, slice_max, batch <= vox::kMaxSeqPerLaunch ? plan : vox::kPlanNone, workspace);
   for (int b0 = 0; b0 < batch; b0 += vox::kMaxSeqPerLaunch) {
     vox::DecodeArgs s = base;
     s.batch = batch - b0 < vox::kMaxSeqPerLaunch ? batch - b0 : vox::kMaxSeqPerLaunch;
@@ -429,6 +436,11 @@ int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const
     d.out_row_stride = out_row_stride;
     d.cu_q = cu_seqlens_q;
     d.cu_k = cu_seqlens_k;
+    if (max_seqlen_q > 1 && vox::mixed_launch_fits(a, num_kv_heads)) {
+      // both kinds of rows in one launch, sharing the CUs (then the merge kernel)
+      const vox::DecodeArgs dw = with_workspace(d, batch, plan, workspace);
+      return hip_status(vox::launch_mixed(a, max_seqlen_q, dw, num_kv_heads, s), "prefill_attn mixed launch");
+    }
     if (max_seqlen_q > 1) {
       const int sp = hip_status(vox::launch_prefill(a, max_seqlen_q, s), "prefill_attn launch");
       if (sp != VOX_OK) return sp;

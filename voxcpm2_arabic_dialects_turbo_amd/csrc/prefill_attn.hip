@@ -29,6 +29,7 @@
 // halves step through the key tiles together). The epilogue multiplies the normalized fp32 o by inv_smooth, takes
 // the per-token max |.| across both halves (LDS atomic max on the float bits, all values >= 0), and writes
 // rint(o / scale) (round half to even) with scale = max(amax, 1e-6) / 127.
+#include "decode_body.h"
 #include "vox_common.h"
 #include "vox_kernels.h"
 
@@ -38,6 +39,7 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kBK = 64;          // keys per tile
+constexpr int kTB = kBK * 256;   // bytes of one K or V tile in LDS (the direct-to-LDS path)
 constexpr int kRows = 128;       // query rows per workgroup (bf16 output)
 // LDS row strides (bf16 elements) of the K and V tiles, chosen by measuring the kernel's own access patterns on
 // gfx950: the K-fragment 16-byte reads run 1.7x faster at 144 than at 136 (and 4-8x faster than at 128 or 132),
@@ -65,9 +67,21 @@ enum KvSource { kPacked = 0, kPagedTiles = 1, kPagedPieces = 2 };
 // NW waves per KV group, each owning RT 16-row blocks of the 128 query rows: 4 waves x 32 rows keep the LDS reads per
 // MFMA low (the largest grids); 8 waves x 16 rows halve each wave's work per key tile, which shortens a workgroup's
 // chain of key tiles (smaller grids, where the longest chains end the launch).
+// The double-buffered K and V tiles of the direct-to-LDS path ([NH] = one per KV-group half), four distinct __shared__
+// arrays of the kernel: the compiler can then tell a tile's reads from the next tile's in-flight DMA writes (a
+// mixed launch's decode workgroups use the same arrays for their own state).
+template <int NH>
+struct DmaBufs {
+  uint8_t (*k0)[kTB];
+  uint8_t (*k1)[kTB];
+  uint8_t (*v0)[kTB];
+  uint8_t (*v1)[kTB];
+};
+
 // One work item: query tile qt of sequence b, kv head gz (QUANT: every kv head, one per half of the workgroup).
 template <bool QUANT, int KV, int NW, int RT>
-__device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b, int gz) {
+__device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b, int gz,
+                                             const DmaBufs<QUANT ? 2 : 1>& bufs) {
   constexpr int NH = QUANT ? 2 : 1;  // KV-group halves per workgroup
   constexpr int ROWS = 16 * RT * NW;  // query rows per KV group
   constexpr int NT = 64 * NW;        // threads per KV group
@@ -373,11 +387,10 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
     // hit 16 different slots) and in slot c ^ 2 (R & 7) in V (the 8 rows under a transposed read's 32 lanes hit 16
     // different slots). The permutation is applied on the global side: the lane that fills slot lc of row R fetches
     // chunk lc ^ f(R).
-    constexpr int kTB = kBK * 256;  // bytes of one tile
-    __shared__ __attribute__((aligned(1024))) uint8_t kt0[NH][kTB];
-    __shared__ __attribute__((aligned(1024))) uint8_t kt1[NH][kTB];
-    __shared__ __attribute__((aligned(1024))) uint8_t vt0[NH][kTB];
-    __shared__ __attribute__((aligned(1024))) uint8_t vt1[NH][kTB];
+    uint8_t (*const kt0)[kTB] = bufs.k0;
+    uint8_t (*const kt1)[kTB] = bufs.k1;
+    uint8_t (*const vt0)[kTB] = bufs.v0;
+    uint8_t (*const vt1)[kTB] = bufs.v1;
     const int lc = lane & 15;
     const int fk = lrow & 15, fv = 2 * (lrow & 7);  // rows PR i + lrow share these
     const uint32_t dk_off = (uint32_t)((lrow * rs_k + ((lc ^ fk) << 3)) * 2);
@@ -653,23 +666,38 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
 // slot: config 2, 832 items on 512 slots, 16.5 -> 13.4 us). Within a rank the (sequence, kv head) pairs rotate by
 // r, so a pair's tiles are dealt over all eight XCDs rather than all landing on one. A form of its own: the extra
 // index arithmetic in the plain grid's kernel cost the short non-causal steps 4-7 %.
-template <bool QUANT, int KV, int NW, int RT, int FORM>
-__global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 : 2) void prefill_kernel(PrefillArgs p) {
-  if constexpr (FORM == kFormRanked) {
-    const int nz = QUANT ? 1 : p.num_kv_heads;  // (QUANT: a workgroup holds every kv head)
-    const int n = p.batch * nz, id = blockIdx.x, r = id / n, c = (id + r) % n;
-    const int qt = p.causal ? (int)gridDim.x / n - 1 - r : r;
-    prefill_tile<QUANT, KV, NW, RT>(p, qt, c / nz, c % nz);
-  } else if constexpr (FORM == kFormPersistent) {
+constexpr int kRankCap = 1024;  // longest sequence, in q tiles, that the persistent rank order covers
+
+// LDS of the persistent walk, for up to `cap` sequences (p.batch <= cap)
+struct ItemLds {
+  int* nt;      // [cap] q tiles of each sequence (0: nothing for this kernel)
+  int* act;     // [cap] the sequences with q tiles, in order
+  int* sorted;  // [cap] ... most tiles first (stable)
+  int* snt;     // [cap] their tile counts
+  int* P;       // [kRankCap + 1] items of the ranks before r
+  int* red;     // [2 x waves]
+  int* first;   // [cap + 1] first item of each sequence (sequence-by-sequence order)
+};
+constexpr int item_lds_ints(int cap, int waves) { return 5 * cap + 1 + kRankCap + 1 + 2 * waves; }
+__device__ __forceinline__ ItemLds item_lds(int* base, int cap, int waves) {
+  return ItemLds{base, base + cap, base + 2 * cap, base + 3 * cap, base + 4 * cap, base + 4 * cap + kRankCap + 1,
+                 base + 4 * cap + kRankCap + 1 + 2 * waves};
+}
+
+// The persistent walk of workgroup g of G (kFormPersistent, and the prefill workgroups of a mixed launch): reads
+// cu_q once, numbers the items of the sequences that have work and walks its share of them (order below).
+template <bool QUANT, int KV, int NW, int RT>
+__device__ __forceinline__ void prefill_items(const PrefillArgs& p, const int g, const int G,
+                                              const DmaBufs<QUANT ? 2 : 1>& bufs, const ItemLds& A) {
+  {
     constexpr int NTH = 64 * NW * (QUANT ? 2 : 1);
     constexpr int ROWS = 16 * RT * NW;
-    constexpr int kRankCap = 1024;  // longest sequence, in q tiles, that the rank order covers
-    __shared__ int s_nt[kMaxSeqPerLaunch];       // q tiles of each sequence (0: nothing for this kernel)
-    __shared__ int s_act[kMaxSeqPerLaunch];      // the sequences with q tiles, in order
-    __shared__ int s_sorted[kMaxSeqPerLaunch];   // ... most tiles first (stable)
-    __shared__ int s_snt[kMaxSeqPerLaunch];      // their tile counts
-    __shared__ int s_P[kRankCap + 1];            // items of the ranks before r
-    __shared__ int s_red[2 * (NTH / 64)];
+    int* const s_nt = A.nt;
+    int* const s_act = A.act;
+    int* const s_sorted = A.sorted;
+    int* const s_snt = A.snt;
+    int* const s_P = A.P;
+    int* const s_red = A.red;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int BQ = ROWS / p.group;
     const int HKz = QUANT ? 1 : p.num_kv_heads;
@@ -735,7 +763,6 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
       }
       __syncthreads();
       const int W = __builtin_amdgcn_readfirstlane(s_P[maxnt]);
-      const int G = gridDim.x, g = blockIdx.x;
       for (int t = 0; t * G < W; ++t) {
         const int k = t * G + ((t & 1) ? G - 1 - g : g);
         if (k >= W) continue;
@@ -747,13 +774,13 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
         const int local = k - __builtin_amdgcn_readfirstlane(s_P[lo]);
         const int bq = __builtin_amdgcn_readfirstlane(s_sorted[local / HKz]);
         const int nt = __builtin_amdgcn_readfirstlane(s_nt[bq]);
-        prefill_tile<QUANT, KV, NW, RT>(p, p.causal ? nt - 1 - lo : lo, bq, local % HKz);
+        prefill_tile<QUANT, KV, NW, RT>(p, p.causal ? nt - 1 - lo : lo, bq, local % HKz, bufs);
         __syncthreads();  // the item's LDS is free for the next one
       }
       return;
     }
-    // sequence-by-sequence order (heaviest causal q tile first within a sequence), every gridDim.x-th item
-    __shared__ int s_first[kMaxSeqPerLaunch + 1];  // first item of each sequence; s_first[batch] = the total
+    // sequence-by-sequence order (heaviest causal q tile first within a sequence), every G-th item
+    int* const s_first = A.first;  // first item of each sequence; s_first[batch] = the total
     run = 0;
     for (int base = 0; base < p.batch; base += NTH) {
       const int bb = base + tid;
@@ -773,7 +800,7 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
     }
     if (tid == 0) s_first[p.batch] = run;
     __syncthreads();
-    for (int i = blockIdx.x; i < run; i += gridDim.x) {
+    for (int i = g; i < run; i += G) {
       int lo = 0, hi = p.batch;  // the last b with s_first[b] <= i (an empty sequence shares the next one's start)
       while (hi - lo > 1) {
         const int mid = (lo + hi) >> 1;
@@ -783,9 +810,30 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
       const int nt = (__builtin_amdgcn_readfirstlane(s_first[lo + 1]) - first) / HKz;
       const int local = i - first;
       const int r = local / HKz;
-      prefill_tile<QUANT, KV, NW, RT>(p, p.causal ? nt - 1 - r : r, lo, local % HKz);
+      prefill_tile<QUANT, KV, NW, RT>(p, p.causal ? nt - 1 - r : r, lo, local % HKz, bufs);
       __syncthreads();  // the item's LDS is free for the next one
     }
+  }
+}
+
+template <bool QUANT, int KV, int NW, int RT, int FORM>
+__global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 : 2) void prefill_kernel(PrefillArgs p) {
+  constexpr int NH = QUANT ? 2 : 1;
+  __shared__ __attribute__((aligned(1024))) uint8_t kt0[NH][kTB];
+  __shared__ __attribute__((aligned(1024))) uint8_t kt1[NH][kTB];
+  __shared__ __attribute__((aligned(1024))) uint8_t vt0[NH][kTB];
+  __shared__ __attribute__((aligned(1024))) uint8_t vt1[NH][kTB];
+  const DmaBufs<NH> bufs{kt0, kt1, vt0, vt1};
+  if constexpr (FORM == kFormRanked) {
+    const int nz = QUANT ? 1 : p.num_kv_heads;  // (QUANT: a workgroup holds every kv head)
+    const int n = p.batch * nz, id = blockIdx.x, r = id / n, c = (id + r) % n;
+    const int qt = p.causal ? (int)gridDim.x / n - 1 - r : r;
+    prefill_tile<QUANT, KV, NW, RT>(p, qt, c / nz, c % nz, bufs);
+  } else if constexpr (FORM == kFormPersistent) {
+    constexpr int NWV = NW * (QUANT ? 2 : 1);
+    __shared__ int s_items[item_lds_ints(kMaxSeqPerLaunch, NWV)];
+    prefill_items<QUANT, KV, NW, RT>(p, (int)blockIdx.x, (int)gridDim.x, bufs,
+                                     item_lds(s_items, kMaxSeqPerLaunch, NWV));
   } else {
     int qt = blockIdx.x, b = blockIdx.y, gz = blockIdx.z;
     if (p.xcd_order) {
@@ -798,8 +846,42 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
       gz = (int)(work / (gridDim.x * gridDim.y));
       if (p.causal) qt = (int)gridDim.x - 1 - qt;  // heavy query tiles first
     }
-    prefill_tile<QUANT, KV, NW, RT>(p, qt, b, gz);
+    prefill_tile<QUANT, KV, NW, RT>(p, qt, b, gz, bufs);
   }
+}
+
+// Mixed prefill + decode step in one launch (a paged varlen call whose one-query rows go to the split-KV decode
+// work): workgroups [0, nd) run decode_split over the one-query rows (da, nd = da.grid workgroups), the others walk
+// the prefill items of the other rows (pa, persistent order, 128-row items). Both roles fit two workgroups per CU
+// (the decode role's state borrows the prefill role's tile buffers: rounds of 3 segments, bf16 slots), so a CU holds
+// one of each and the prefill rows' MFMA and LDS work runs beside the decode rows' memory stream instead of after it
+// (the dispatcher places workgroups [0, nd) one per CU, then the rest in the second slots: read back from HW_ID in a
+// working probe). One 4-wave workgroup shape, paged tiles (block_size a multiple of 64), at most 256 sequences.
+template <int HK>
+__global__ __launch_bounds__(256, 2) void mixed_kernel(PrefillArgs pa, DecodeArgs da) {
+  using LB = dec::LdsBorrowed<HK>;
+  static_assert(LB::kBufBytes == kTB, "the decode role borrows the prefill tile buffers");
+  constexpr int kItemInts = item_lds_ints(LB::kSeqCap, 4);
+  constexpr int kAux = LB::kAuxBytes > kItemInts * 4 ? LB::kAuxBytes : kItemInts * 4;
+  __shared__ __attribute__((aligned(1024))) uint8_t kt0[1][kTB];
+  __shared__ __attribute__((aligned(1024))) uint8_t kt1[1][kTB];
+  __shared__ __attribute__((aligned(1024))) uint8_t vt0[1][kTB];
+  __shared__ __attribute__((aligned(1024))) uint8_t vt1[1][kTB];
+  __shared__ __attribute__((aligned(16))) uint8_t aux[kAux];
+  const int nd = da.grid;
+  if ((int)blockIdx.x < nd) {
+    const LB L(kt0[0], kt1[0], vt0[0], vt1[0], aux);
+    dec::decode_split<HK>(da, (int)blockIdx.x, nd, L);
+    return;
+  }
+  // The prefill rows are the longer pole (alone on the CUs they would take 2x the time they take at two workgroups
+  // per CU), the decode rows a memory stream that tolerates waiting: the prefill waves issue first (config 5, the
+  // attention call: 53.6 -> 49.6 us), and take 128-row items (4 waves x 32 rows), which halve the key-tile steps of
+  // the 64-row items for the same LDS (49.6 -> 44.0 us).
+  __builtin_amdgcn_s_setprio(1);
+  const DmaBufs<1> bufs{kt0, kt1, vt0, vt1};
+  prefill_items<false, kPagedTiles, 4, 2>(pa, (int)blockIdx.x - nd, (int)gridDim.x - nd, bufs,
+                                           item_lds(reinterpret_cast<int*>(aux), LB::kSeqCap, 4));
 }
 
 }  // namespace
@@ -824,6 +906,30 @@ hipError_t launch_prefill_kind(const PrefillArgs& a, dim3 grid, hipStream_t stre
   else
     prefill_kernel<QUANT, kPagedPieces, NW, RT, FORM><<<grid, block, 0, stream>>>(a);
   return hipGetLastError();
+}
+
+bool mixed_launch_fits(const PrefillArgs& a, int num_kv_heads) {
+  return a.cu_q && a.block_tables && a.block_size % kBK == 0 && a.group > 0 && kRows % a.group == 0 &&
+         a.batch >= 1 && a.batch <= dec::LdsBorrowed<2>::kSeqCap && (num_kv_heads == 1 || num_kv_heads == 2);
+}
+
+hipError_t launch_mixed(const PrefillArgs& a, int max_seqlen_q, const DecodeArgs& d, int num_kv_heads,
+                        hipStream_t stream) {
+  if (!mixed_launch_fits(a, num_kv_heads) || d.batch != a.batch || d.grid < 1 || max_seqlen_q <= 0)
+    return hipErrorInvalidValue;
+  // the prefill workgroups: at most one per 128-row item, and one per CU (the other slot of each CU holds a decode
+  // workgroup; a third of them more, waiting for free slots, measured slower: 49.6 -> 57.2 us)
+  const int64_t bq = kRows / a.group;
+  const int64_t items = ((int64_t)max_seqlen_q + bq - 1) / bq * a.batch * a.num_kv_heads;
+  const int64_t np = items < device_cus() ? items : device_cus();
+  const dim3 grid((unsigned)(d.grid + np)), block(256);
+  if (num_kv_heads == 1)
+    mixed_kernel<1><<<grid, block, 0, stream>>>(a, d);
+  else
+    mixed_kernel<2><<<grid, block, 0, stream>>>(a, d);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_decode_merge(d, stream);
 }
 
 hipError_t launch_prefill(const PrefillArgs& a0, int max_seqlen_q, hipStream_t stream) {

@@ -114,8 +114,17 @@ hipError_t launch_store_kvcache(const void* k, const void* v, int64_t k_row_stri
                                 int64_t n, int row_elems, bool vec16, hipStream_t stream);
 
 hipError_t launch_decode(const DecodeArgs& a, int num_kv_heads, hipStream_t stream);
+// The merge kernel alone (after a mixed launch whose decode workgroups left partials).
+hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream);
 
 hipError_t launch_prefill(const PrefillArgs& a, int max_seqlen_q, hipStream_t stream);
+
+// A mixed prefill + decode step as one launch: the one-query rows on decode workgroups (d, its workspace set up),
+// the other rows on persistent prefill workgroups (a, persistent with skip_single) sharing the CUs, then the merge
+// kernel. For the shapes mixed_launch_fits accepts (paged tiles, at most 256 sequences).
+bool mixed_launch_fits(const PrefillArgs& a, int num_kv_heads);
+hipError_t launch_mixed(const PrefillArgs& a, int max_seqlen_q, const DecodeArgs& d, int num_kv_heads,
+                        hipStream_t stream);
 
 hipError_t launch_copy_block_prefix(const CopyArgs& a, int max_tokens, bool vec16, hipStream_t stream);
 
