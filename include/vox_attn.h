@@ -133,7 +133,8 @@ void vox_set_decode_workgroups(int workgroups);
  *                  decode rows of a mixed prefill + decode step) then run on the split-KV decode kernel, which spreads
  *                  long contexts over every CU (needs num_heads <= 16, num_kv_heads 1 or 2, block_size a multiple of
  *                  32, out 16-byte aligned with out_row_stride a multiple of 8; otherwise, or with NULL, the prefill
- *                  kernel takes every row). Same results either way.
+ *                  kernel takes every row). Calls of up to 256 sequences over blocks of a multiple of 64 tokens run
+ *                  both kinds of rows in one launch, sharing every CU. Results within the same tolerance either way.
  * Supported: head_dim 128, num_heads / num_kv_heads dividing 128. */
 int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const void* value,
                      int64_t key_row_stride, int64_t value_row_stride, const void* k_cache, const void* v_cache,
