@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define VOX_ABI_VERSION 9
+#define VOX_ABI_VERSION 10
 
 #define VOX_OK 0
 #define VOX_EINVAL 1 /* bad argument: shape, stride, alignment or null pointer (reference: the asserts of
@@ -147,6 +147,21 @@ int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const
 /* Scratch bytes vox_prefill_attn's one-query rows need for `batch` sequences on the current device. No reference
  * counterpart (flash-attn sizes its buffers internally; reference call site: nanovllm_voxcpm/model/layers.py:337). */
 size_t vox_prefill_workspace_bytes(int batch);
+
+/* A packed prefill step's KV store and its attention in one call: vox_store_kvcache(key, value, key_row_stride,
+ * value_row_stride, k_cache, v_cache, num_slots, slot_mapping, num_tokens, num_kv_heads, head_dim) followed by
+ * vox_prefill_attn over the packed rows key / value (no block table) (reference: the prefill branch of
+ * nanovllm_voxcpm/model/layers.py:326-348 without a block table, store_kvcache then flash_attn_varlen_func over the
+ * step's own k and v). The attention reads the packed rows, not the cache, so the copy rides in the attention launch
+ * (the last workgroups copy the rows after their own work) instead of a launch of its own. Outputs and caches are
+ * identical to the two calls. Rows the 16-byte copy cannot move (16-byte aligned rows, strides multiples of 8) take
+ * the two calls. Arguments as in those two functions; num_tokens = the rows of key / value and slot_mapping. */
+int vox_prefill_attn_store(const void* q, int64_t q_row_stride, const void* key, const void* value,
+                           int64_t key_row_stride, int64_t value_row_stride, const int32_t* slot_mapping,
+                           void* k_cache, void* v_cache, int64_t num_slots, int64_t num_tokens,
+                           const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch, int max_seqlen_q,
+                           int num_heads, int num_kv_heads, int head_dim, float softmax_scale, int causal, void* out,
+                           int64_t out_row_stride, void* stream);
 
 /* vox_prefill_attn with the int8 output epilogue the W8A8 o_proj consumes. Replaces the quant=True modes of the
  * Triton paged_prefill_attention, short_causal_attention and short_attention (reference:

@@ -146,6 +146,26 @@ def test_prefill_rejects_bad_arguments():
     assert lib.vox_prefill_attn(*zero) == _lib.VOX_OK
 
 
+def test_prefill_store_rejects_bad_arguments_before_launching():
+    """The packed prefill with the store riding in it checks every argument of both parts before it launches
+    anything; nothing to attend and nothing to store is a no-op."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    # q, q stride, key, value, key/value strides, slots, k/v cache, num_slots, num_tokens, cu_q, cu_k, batch,
+    # max_seqlen_q, H, HK, D, scale, causal, out, out stride, stream (fake pointers: never passed unmodified)
+    args = [p, 2560, p, p, 2560, 2560, p, p, p, 1 << 17, 100, p, p, 2, 64, 16, 2, 128, 0.088, 1, p, 2048, None]
+    for i, val, msg in [(17, 64, "head_dim"), (2, None, "null"), (6, None, "null"), (11, None, "null"),
+                        (4, 200, "row strides"), (9, 0, "empty cache"), (13, -1, "negative"), (10, -5, "negative"),
+                        (20, None, "null out"), (21, 100, "out row stride"), (16, 3, "multiple")]:
+        bad = list(args)
+        bad[i] = val
+        assert lib.vox_prefill_attn_store(*bad) == _lib.VOX_EINVAL, (i, val)
+        assert msg in _err(), (i, val, _err())
+    empty = list(args)
+    empty[13], empty[10] = 0, 0  # no sequences, no rows
+    assert lib.vox_prefill_attn_store(*empty) == _lib.VOX_OK
+
+
 def test_prefill_int8_rejects_bad_arguments():
     lib = _lib.load()
     p = ctypes.c_void_p(256)

@@ -163,7 +163,7 @@ class _Recorder:
     def __init__(self, monkeypatch):
         self.calls = []
         for name in ("store_kvcache", "flash_attn_varlen_func", "flash_attn_with_kvcache", "flash_attn_func",
-                     "decode_attention"):
+                     "decode_attention", "prefill_attention_store"):
             monkeypatch.setattr(layers, name, self._make(name))
 
     def _make(self, name):
@@ -173,7 +173,9 @@ class _Recorder:
         return fn
 
 
-def test_prefill_without_prefix_attends_over_the_step_kv(monkeypatch):
+def test_prefill_without_prefix_stores_and_attends_over_the_step_kv_in_one_call(monkeypatch):
+    """store_kvcache then flash_attn_varlen_func over the step's own k / v (reference layers.py:332-348): the
+    attention reads the packed rows, so the store rides in the same call."""
     rec = _Recorder(monkeypatch)
     attn = Attention(16, 128, 0.125, 2)
     attn.k_cache, attn.v_cache = torch.zeros(2, 256, 2, 128), torch.zeros(2, 256, 2, 128)
@@ -182,11 +184,10 @@ def test_prefill_without_prefix_attends_over_the_step_kv(monkeypatch):
     slots = torch.arange(5, dtype=torch.int32)
     set_context(True, cu, cu, 5, 5, slots, None, None)
     assert attn(q, k, v) == "o"
-    (n0, a0, _), (n1, a1, kw1) = rec.calls
-    assert n0 == "store_kvcache" and a0[0] is k and a0[2] is attn.k_cache and a0[4] is slots
-    assert n1 == "flash_attn_varlen_func" and a1[1] is k and a1[2] is v
-    assert kw1 == dict(max_seqlen_q=5, cu_seqlens_q=cu, max_seqlen_k=5, cu_seqlens_k=cu, softmax_scale=0.125,
-                       causal=True, block_table=None)
+    ((n0, a0, kw0),) = rec.calls
+    assert n0 == "prefill_attention_store" and a0[0] is q and a0[1] is k and a0[2] is v
+    assert a0[3] is attn.k_cache and a0[4] is attn.v_cache and a0[5] is slots
+    assert kw0 == dict(cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=5, softmax_scale=0.125, causal=True)
 
 
 def test_prefill_with_block_tables_reads_the_caches(monkeypatch):

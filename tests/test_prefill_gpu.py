@@ -601,3 +601,46 @@ def test_mixed_launch_plan_recorded_then_reused_equals_unplanned():
         assert torch.equal(o, plain), f"call {i} ({'record' if i == 0 else 'reuse'}) differs from the unplanned one"
     want = ref.varlen(q.float().cpu(), _cu(nq), _cu(nk), k_cache=kc, v_cache=vc, block_tables=tables)
     attn_close(plain, want, "mixed launch, planned")
+
+
+@pytest.mark.parametrize("case", ["config2", "short", "padded_slots", "one_kv_head", "unaligned_caches"])
+def test_packed_prefill_with_the_store_riding_in_it_equals_store_then_prefill(case):
+    """prefill_attention_store (the store copied by the attention launch's last workgroups) against store_kvcache
+    then the packed varlen prefill on the same inputs: outputs and both caches bit-identical, the outputs within
+    tolerance of the oracle. Cases: config 2 (8 x U[64, 512]); many short sequences (a grid of fewer than 256
+    workgroups, each copying several rows); padding slots (-1) and slots past the cache, which store nothing;
+    one kv head; caches that are not 16-byte aligned (the two-call form)."""
+    from voxcpm2_arabic_dialects_turbo_amd.ops import prefill_attention_store
+
+    gen = torch.Generator().manual_seed(96)
+    hk = 1 if case == "one_kv_head" else HK
+    lens = uniform_lens(gen, 40, 1, 30) if case == "short" else uniform_lens(gen, 8, 64, 512)
+    T = sum(lens)
+    kc, vc, tables = paged_pool(gen, lens, 512, hk=hk)
+    qkv = randn(gen, T, (H + 2 * hk) * D).to(DEV)
+    q, k, v = qkv.split([H * D, hk * D, hk * D], dim=-1)
+    q, k, v = q.view(T, H, D), k.view(T, hk, D), v.view(T, hk, D)
+    slots = torch.cat([torch.tensor([ref.slot_of(tables[b].tolist(), j, BLOCK) for j in range(n)])
+                       for b, n in enumerate(lens)]).to(torch.int32)
+    if case == "padded_slots":
+        slots[::7] = -1
+        slots[3::11] = 512 * BLOCK + 5  # past the cache
+    cu = _cu(lens).to(DEV)
+    kc1, vc1 = kc.to(DEV), vc.to(DEV)
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    if case == "unaligned_caches":  # the same caches 8 bytes into their buffers
+        def shifted(c):
+            buf = torch.empty(c.numel() + 4, dtype=c.dtype, device=DEV)
+            view = buf[4:].view(c.shape)
+            view.copy_(c)
+            return view
+        kc1, vc1 = shifted(kc1), shifted(vc1)
+    fused = prefill_attention_store(q, k, v, kc1, vc1, slots.to(DEV), cu_seqlens_q=cu, cu_seqlens_k=cu,
+                                    max_seqlen_q=max(lens), softmax_scale=SCALE)
+    store_kvcache(k, v, kc2, vc2, slots.to(DEV))
+    two = flash_attn_varlen_func(q, k, v, cu, cu, max(lens), max(lens), softmax_scale=SCALE, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, two), f"{case}: outputs differ from store + prefill"
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2), f"{case}: caches differ from store_kvcache's"
+    want = ref.varlen(q.float().cpu(), _cu(lens), _cu(lens), k=k.cpu(), v=v.cpu())
+    attn_close(fused, want, f"{case}: against the oracle")

@@ -450,6 +450,55 @@ int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const
   return hip_status(vox::launch_prefill(a, max_seqlen_q, s), "prefill_attn launch");
 }
 
+int vox_prefill_attn_store(const void* q, int64_t q_row_stride, const void* key, const void* value,
+                           int64_t key_row_stride, int64_t value_row_stride, const int32_t* slot_mapping,
+                           void* k_cache, void* v_cache, int64_t num_slots, int64_t num_tokens,
+                           const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch, int max_seqlen_q,
+                           int num_heads, int num_kv_heads, int head_dim, float softmax_scale, int causal, void* out,
+                           int64_t out_row_stride, void* stream) {
+  if (batch < 0 || max_seqlen_q < 0 || num_tokens < 0)
+    return fail(VOX_EINVAL, "prefill_attn_store: negative batch, max_seqlen_q or num_tokens");
+  if (!key || !value || !k_cache || !v_cache || !slot_mapping || !cu_seqlens_q || !cu_seqlens_k)
+    return fail(VOX_EINVAL, "prefill_attn_store: null pointer argument");
+  if (num_slots <= 0) return fail(VOX_EINVAL, "prefill_attn_store: empty cache");
+  const int64_t row = (int64_t)num_kv_heads * head_dim;
+  if (num_kv_heads <= 0 || head_dim <= 0 || key_row_stride < row || value_row_stride < row)
+    return fail(VOX_EINVAL, "prefill_attn_store: key / value row strides smaller than num_kv_heads * head_dim");
+  // every argument is checked before anything is launched
+  const bool attend = batch > 0 && max_seqlen_q > 0;
+  vox::PrefillArgs a;
+  if (attend) {
+    if (!out) return fail(VOX_EINVAL, "prefill_attn_store: null out");
+    if (out_row_stride < (int64_t)num_heads * head_dim || out_row_stride % 4 || ((uintptr_t)out & 7u))
+      return fail(VOX_EINVAL, "prefill_attn_store: bad out row stride or alignment");
+    const int st = prefill_setup("prefill_attn_store", q, q_row_stride, key, value, key_row_stride,
+                                 value_row_stride, nullptr, nullptr, 0, 0, nullptr, 0, 0, cu_seqlens_q, cu_seqlens_k,
+                                 batch, max_seqlen_q, 0, 0, num_heads, num_kv_heads, head_dim, softmax_scale, causal,
+                                 &a);
+    if (st != VOX_OK) return st;
+  }
+  const bool vec16 = row % 8 == 0 && key_row_stride % 8 == 0 && value_row_stride % 8 == 0 && aligned16(key) &&
+                     aligned16(value) && aligned16(k_cache) && aligned16(v_cache);
+  if (!attend || !vec16 || num_tokens == 0) {
+    // no launch to ride in, nothing to store, or rows the 16-byte copy cannot move: the two calls
+    const int st = vox_store_kvcache(key, value, key_row_stride, value_row_stride, k_cache, v_cache, num_slots,
+                                     slot_mapping, num_tokens, num_kv_heads, head_dim, stream);
+    if (st != VOX_OK || !attend) return st;
+    return vox_prefill_attn(q, q_row_stride, key, value, key_row_stride, value_row_stride, nullptr, nullptr, 0, 0,
+                            nullptr, 0, 0, cu_seqlens_q, cu_seqlens_k, batch, max_seqlen_q, 0, 0, num_heads,
+                            num_kv_heads, head_dim, softmax_scale, causal, out, out_row_stride, VOX_PLAN_NONE,
+                            nullptr, 0, stream);
+  }
+  a.out = (uint16_t*)out;
+  a.out_row_stride = out_row_stride;
+  a.store_slots = slot_mapping;
+  a.store_k_cache = (uint16_t*)k_cache;
+  a.store_v_cache = (uint16_t*)v_cache;
+  a.store_rows = num_tokens;
+  a.store_num_slots = num_slots;
+  return hip_status(vox::launch_prefill(a, max_seqlen_q, (hipStream_t)stream), "prefill_attn_store launch");
+}
+
 int vox_prefill_attn_int8(const void* q, int64_t q_row_stride, const void* key, const void* value,
                           int64_t key_row_stride, int64_t value_row_stride, const void* k_cache, const void* v_cache,
                           int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,

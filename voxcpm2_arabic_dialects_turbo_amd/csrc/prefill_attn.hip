@@ -816,6 +816,46 @@ __device__ __forceinline__ void prefill_items(const PrefillArgs& p, const int g,
   }
 }
 
+// The KV store riding in a packed launch (PrefillArgs::store_rows; what store_kvcache_kernel does): workgroup wid of
+// the store_wgs copying ones copies rows wid, wid + store_wgs, ..., 16 bytes per lane, every load of a batch issued
+// before its stores. Nothing in a packed launch reads the cache, so the copy may run anywhere in it. It runs after
+// the workgroup's item (before it, the item's first wait also waited for the copy's stores: config 2 step 13.3 ->
+// 14.3 us), in workgroups [256, 512) of the launch order: at config 2 the rank-major grid's medium items, resident
+// from the start and done well before the heaviest chains (the grid's last 256, dispatched last, 13.9 us; here
+// 13.3 us, the time of the launch without the store).
+__device__ __forceinline__ void store_rows(const PrefillArgs& p, int wid) {
+  const int row = p.num_kv_heads * kD;  // elements of one K (or V) row
+  const int pieces = row / 8;           // 16-byte pieces per row
+  const int per_row = 2 * pieces;
+  const int64_t rows = (p.store_rows - wid + p.store_wgs - 1) / p.store_wgs;
+  const int64_t total = rows * per_row;
+  const int nth = (int)blockDim.x;
+  constexpr int kBatch = 4;
+  for (int64_t base = threadIdx.x; base < total; base += (int64_t)kBatch * nth) {
+    u32x4 val[kBatch];
+    int64_t slot[kBatch];
+    uint16_t* dst[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t idx = base + (int64_t)u * nth;
+      const bool in = idx < total;
+      const int64_t r_local = in ? idx / per_row : 0;
+      const int rem = (int)(idx - r_local * per_row);
+      const int which = rem >= pieces;  // 0: key, 1: value
+      const int piece = rem - which * pieces;
+      const int64_t tok = wid + r_local * p.store_wgs;
+      const uint16_t* src = (which ? p.v_src + tok * p.v_row_stride : p.k_src + tok * p.k_row_stride) + piece * 8;
+      val[u] = in ? ld_g16(src) : zero4();
+      slot[u] = in ? (int64_t)p.store_slots[tok] : -1;
+      dst[u] = (which ? p.store_v_cache : p.store_k_cache) + piece * 8;
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (slot[u] >= 0 && slot[u] < p.store_num_slots)
+        *reinterpret_cast<u32x4*>(dst[u] + slot[u] * row) = val[u];
+  }
+}
+
 template <bool QUANT, int KV, int NW, int RT, int FORM>
 __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 : 2) void prefill_kernel(PrefillArgs p) {
   constexpr int NH = QUANT ? 2 : 1;
@@ -829,6 +869,8 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
     const int n = p.batch * nz, id = blockIdx.x, r = id / n, c = (id + r) % n;
     const int qt = p.causal ? (int)gridDim.x / n - 1 - r : r;
     prefill_tile<QUANT, KV, NW, RT>(p, qt, c / nz, c % nz, bufs);
+    if constexpr (KV == kPacked && !QUANT)
+      if (p.store_rows > 0 && id >= p.store_first && id < p.store_first + p.store_wgs) store_rows(p, id - p.store_first);
   } else if constexpr (FORM == kFormPersistent) {
     constexpr int NWV = NW * (QUANT ? 2 : 1);
     __shared__ int s_items[item_lds_ints(kMaxSeqPerLaunch, NWV)];
@@ -847,6 +889,12 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
       if (p.causal) qt = (int)gridDim.x - 1 - qt;  // heavy query tiles first
     }
     prefill_tile<QUANT, KV, NW, RT>(p, qt, b, gz, bufs);
+    if constexpr (KV == kPacked && !QUANT) {
+      if (p.store_rows > 0) {
+        const int id = (int)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
+        if (id >= p.store_first && id < p.store_first + p.store_wgs) store_rows(p, id - p.store_first);
+      }
+    }
   }
 }
 
@@ -933,6 +981,7 @@ hipError_t launch_mixed(const PrefillArgs& a, int max_seqlen_q, const DecodeArgs
 }
 
 hipError_t launch_prefill(const PrefillArgs& a0, int max_seqlen_q, hipStream_t stream) {
+  if (a0.store_rows > 0 && (a0.block_tables || a0.persistent || !a0.store_slots)) return hipErrorInvalidValue;
   if (max_seqlen_q <= 0 || a0.batch <= 0) return hipSuccess;
   PrefillArgs a = a0;
   if (a.persistent) {
@@ -960,11 +1009,18 @@ hipError_t launch_prefill(const PrefillArgs& a0, int max_seqlen_q, hipStream_t s
   // (config 2: 16.9 -> 16.2 us), while on short sequences the doubled tile loads cost more than that saves (44 x 46
   // tokens paged 12.8 -> 14.0 us, LocDiT 150 x 11 8.4 -> 10.0 us with the wider rule). A causal grid beyond two per
   // CU runs rank-major (heaviest q tiles first).
+  // a riding KV store (packed keys only) is copied by min(grid, 256) workgroups: [256, 512) in launch order, or the
+  // last ones of a smaller grid
+  auto store_by = [&](int64_t nwg) {
+    a.store_wgs = a.store_rows > 0 ? (int)(nwg < 256 ? nwg : 256) : 0;
+    a.store_first = (int)(nwg - a.store_wgs < 256 ? nwg - a.store_wgs : 256);
+  };
   const bool fits64 = 64 % a.group == 0;  // group sizes above 64 take the 128-row form only
   const int64_t tiles64 = fits64 ? (max_seqlen_q + 64 / a.group - 1) / (64 / a.group) : 0;
   const int64_t grid64 = tiles64 * a.batch * a.num_kv_heads, cus = device_cus();
   if (fits64 && (grid64 <= 2 * cus || (grid64 <= 4 * cus && tiles64 >= 16))) {
     a.xcd_order = 0;
+    store_by(grid64);
     if (a.causal && grid64 > 2 * cus && grid64 <= INT32_MAX)
       return launch_prefill_kind<false, 4, 1, kFormRanked>(a, dim3((unsigned)grid64), stream);
     return launch_prefill_kind<false, 4, 1>(a, dim3((unsigned)tiles64, (unsigned)a.batch, (unsigned)a.num_kv_heads),
@@ -974,6 +1030,7 @@ hipError_t launch_prefill(const PrefillArgs& a0, int max_seqlen_q, hipStream_t s
   const int q_tiles = (max_seqlen_q + bq - 1) / bq;
   const int64_t nwg = (int64_t)q_tiles * a.batch * a.num_kv_heads;
   a.xcd_order = nwg >= kXcdOrderMinWorkgroups;
+  store_by(nwg);
   const dim3 grid((unsigned)q_tiles, (unsigned)a.batch, (unsigned)a.num_kv_heads);
   if (nwg <= kSmallGridWorkgroups) return launch_prefill_kind<false, 8, 1>(a, grid, stream);
   return launch_prefill_kind<false, 4, 2>(a, grid, stream);

@@ -97,6 +97,17 @@ struct PrefillArgs {
                               // sequences, found by a scan of cu_q (at most kMaxSeqPerLaunch sequences per launch)
   int64_t row_limit;          // > 0: output rows at or past it are neither read (q) nor written (the rows the caller's
                               // output holds; a cu_seqlens_q reaching past it truncates instead of writing out of bounds)
+  // KV store riding in a packed launch (vox_prefill_attn_store): rows i < store_rows of k_src / v_src go to cache slot
+  // store_slots[i] of store_k_cache / store_v_cache (rows of num_kv_heads * 128; -1 and slots outside
+  // [0, store_num_slots) skipped), copied by workgroups [store_first, store_first + store_wgs) (launch order) after
+  // their work item
+  const int32_t* store_slots;
+  uint16_t* store_k_cache;
+  uint16_t* store_v_cache;
+  int64_t store_rows;         // 0: no store
+  int64_t store_num_slots;
+  int store_first;
+  int store_wgs;
 };
 
 struct CopyArgs {

@@ -26,7 +26,7 @@ from torch import nn
 
 from .context import get_context
 from .ops import (decode_attention, flash_attn_func, flash_attn_varlen_func, flash_attn_with_kvcache, planning,
-                  store_kvcache)
+                  prefill_attention_store, store_kvcache)
 
 __all__ = ["Attention", "store_kvcache"]
 
@@ -95,6 +95,14 @@ class Attention(nn.Module):
                 return decode_attention(q, k_cache, v_cache, context.context_lens, context.block_tables, self.scale,
                                         key=k, value=v, slot_mapping=context.slot_mapping,
                                         plan=_plan_key(context)).unsqueeze(1)
+            if cached and context.is_prefill and context.block_tables is None and context.cu_seqlens_q is not None \
+                    and context.slot_mapping is not None:
+                # prefill over the step's own rows: the store rides in the attention launch, which reads the packed
+                # rows rather than the cache
+                return prefill_attention_store(q, k, v, k_cache, v_cache, context.slot_mapping,
+                                               cu_seqlens_q=context.cu_seqlens_q, cu_seqlens_k=context.cu_seqlens_k,
+                                               max_seqlen_q=context.max_seqlen_q, softmax_scale=self.scale,
+                                               causal=True)
             if cached:
                 store_kvcache(k, v, k_cache, v_cache, context.slot_mapping)
             if context.is_prefill:

@@ -341,6 +341,49 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor | None, v: torch.Tensor | 
     return out
 
 
+def prefill_attention_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
+                            v_cache: torch.Tensor, slot_mapping: torch.Tensor, *, cu_seqlens_q: torch.Tensor,
+                            cu_seqlens_k: torch.Tensor, max_seqlen_q: int, softmax_scale: float, causal: bool = True,
+                            out: torch.Tensor | None = None) -> torch.Tensor:
+    """store_kvcache(k, v, k_cache, v_cache, slot_mapping) then the packed varlen attention over k / v, as one call
+    (vox_prefill_attn_store: the copy rides in the attention launch, which reads the packed rows, not the cache).
+    Same outputs and caches as the two calls. Reference: the prefill branch of nanovllm_voxcpm/model/layers.py:
+    326-348 without a block table."""
+    T, H, D = q.shape
+    N, HK, Dk = k.shape
+    _require(k.stride(-1) == 1 and v.stride(-1) == 1, "key/value: last dim must be contiguous")
+    _require(k.stride(1) == Dk and v.stride(1) == Dk, "key/value: heads must be head_dim apart")
+    _require(k_cache.stride(1) == HK * Dk and v_cache.stride(1) == HK * Dk,
+             "caches: slot rows must be num_kv_heads*head_dim apart")
+    _require(slot_mapping.numel() == N, "slot_mapping must hold one slot per token")
+    dev = _check_cuda(q, k, v, k_cache, v_cache, slot_mapping, cu_seqlens_q, cu_seqlens_k)
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16 \
+            or k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
+        raise TypeError("prefill_attention_store takes bf16 q, k, v and caches")
+    if D != HEAD_DIM or Dk != HEAD_DIM or q.stride(2) != 1 or q.stride(1) != D or v.shape != k.shape:
+        raise ValueError(f"q / k / v must be [T, H, {HEAD_DIM}] / [N, HK, {HEAD_DIM}] with contiguous heads")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()) or k_cache.shape != v_cache.shape:
+        raise ValueError("caches must be contiguous [num_blocks, block_size, HK, head_dim] of one shape")
+    if H % HK:
+        raise ValueError(f"num_heads {H} is not a multiple of num_kv_heads {HK}")
+    B = cu_seqlens_q.numel() - 1
+    if cu_seqlens_k.numel() != B + 1:
+        raise ValueError("cu_seqlens_k must have as many entries as cu_seqlens_q")
+    cu_q = _as_i32(cu_seqlens_q, "cu_seqlens_q")
+    cu_k = _as_i32(cu_seqlens_k, "cu_seqlens_k")
+    slots = _as_i32(slot_mapping.reshape(-1), "slot_mapping")
+    if out is None:
+        out = torch.empty(T, H, D, dtype=q.dtype, device=dev)
+    lib = _lib.load()
+    _lib.check(lib.vox_prefill_attn_store(q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(), k.stride(0),
+                                          v.stride(0), slots.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                          k_cache.numel() // (HK * Dk), N, cu_q.data_ptr(), cu_k.data_ptr(), max(B, 0),
+                                          int(max_seqlen_q) if T else 0, H, HK, D, float(softmax_scale),
+                                          1 if causal else 0, out.data_ptr(), out.stride(0), _lib.stream_handle(dev)),
+               "prefill_attn_store")
+    return out
+
+
 # --------------------------------------------------------------------------------------------------------------------
 # The flash-attn entry points the reference's Attention.forward calls
 #
