@@ -305,3 +305,51 @@ def test_int8_output_rows_past_num_tokens_are_never_written(two_pass, monkeypatc
         full_q, full_s = varlen_attention(q, k, v, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=max(lens),
                                           softmax_scale=SCALE, causal=True, quant=True)
     assert torch.equal(out_q[:cut * H * D].view(cut, H * D), full_q[:cut]) and torch.equal(out_s[:cut], full_s[:cut])
+
+
+@pytest.mark.parametrize("h,hk,smooth", [(16, 2, False), (16, 2, True), (16, 1, True)])
+def test_int8_two_pass_codes_equal_the_quantized_bf16_output(h, hk, smooth):
+    """The two-pass form of the long causal shapes (the bf16 kernel into the workspace, then the per-token
+    quantization) quantizes the bf16 output the plain call gives, bit for bit: codes and scales equal the oracle's
+    quantization of that output (config-2-like lengths)."""
+    gen = torch.Generator().manual_seed(85 + h + hk)
+    lens = [412, 393, 361, 205, 108, 405, 75, 74]
+    T = sum(lens)
+    lib = _lib.load()
+    assert lib.vox_prefill_int8_workspace_bytes(T, len(lens), max(lens), h, hk, D, 1) > 0
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device=DEV)
+    q, k, v = (randn(gen, T, n, D).to(DEV) for n in (h, hk, hk))
+    inv = (torch.rand(h * D, generator=gen) + 0.5).to(DEV) if smooth else None
+    kw = dict(cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=max(lens), softmax_scale=SCALE, causal=True)
+    codes, scales = varlen_attention(q, k, v, quant=True, inv_smooth=inv, **kw)
+    o = varlen_attention(q, k, v, **kw)
+    torch.cuda.synchronize()
+    q_ref, s_ref = ref.quantize_rows(o.reshape(T, -1).float().cpu(), None if inv is None else inv.cpu())
+    assert torch.equal(scales.cpu(), s_ref), "scales differ from the quantized bf16 output's"
+    assert torch.equal(codes.cpu(), q_ref), "codes differ from the quantized bf16 output's"
+
+
+def test_int8_two_pass_in_a_hip_graph_replays_like_eager():
+    """The two-pass int8 form captured in a HIP graph (its workspace allocated inside the capture) and replayed four
+    times, with eager calls on other inputs between the replays: every replay equals the eager result bit for bit."""
+    gen = torch.Generator().manual_seed(86)
+    lens = [333, 150, 271, 500, 9, 310]
+    T = sum(lens)
+    assert _lib.load().vox_prefill_int8_workspace_bytes(T, len(lens), max(lens), H, HK, D, 1) > 0
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device=DEV)
+    q, k, v = (randn(gen, T, n, D).to(DEV) for n in (H, HK, HK))
+    q2 = randn(gen, T, H, D).to(DEV)
+    kw = dict(cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=max(lens), softmax_scale=SCALE, causal=True, quant=True)
+    eager = varlen_attention(q, k, v, **kw)
+    eager2 = varlen_attention(q2, k, v, **kw)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        static = varlen_attention(q, k, v, **kw)
+    for r in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static[0], eager[0]) and torch.equal(static[1], eager[1]), f"replay {r}"
+        other = varlen_attention(q2, k, v, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(other[0], eager2[0]) and torch.equal(other[1], eager2[1])
