@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define VOX_ABI_VERSION 10
+#define VOX_ABI_VERSION 11
 
 #define VOX_OK 0
 #define VOX_EINVAL 1 /* bad argument: shape, stride, alignment or null pointer (reference: the asserts of
@@ -162,6 +162,29 @@ int vox_prefill_attn_store(const void* q, int64_t q_row_stride, const void* key,
                            const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch, int max_seqlen_q,
                            int num_heads, int num_kv_heads, int head_dim, float softmax_scale, int causal, void* out,
                            int64_t out_row_stride, void* stream);
+
+/* A paged prefill step's KV store and its attention in one call: vox_store_kvcache(key, value, key_row_stride,
+ * value_row_stride, k_cache, v_cache, num_blocks * block_size, slot_mapping, num_tokens, num_kv_heads, head_dim)
+ * followed by vox_prefill_attn over the caches through block_tables (reference: the prefill branch of
+ * nanovllm_voxcpm/model/layers.py:326-348 with a block table, store_kvcache then flash_attn_varlen_func over
+ * k_cache / v_cache; the mixed steps of nanovllm_voxcpm/engine/scheduler.py:340 (_ride) take this branch).
+ * When the call runs as one mixed launch (vox_prefill_attn's conditions: workspace, up to 256 sequences, blocks of a
+ * multiple of 64 tokens, some sequence with more than one query) and the rows are 16-byte aligned with strides
+ * multiples of 8 (below 2^24 elements), the store rides in it: each sequence's new keys (its last nq key positions) are
+ * read from the rows key / value (row cu_seqlens_q[b] + i for the i-th) instead of the cache, and the merge kernel
+ * writes every row into the caches after the reads. That equals the two calls when, as the engine's scheduler
+ * guarantees, slot_mapping holds for each sequence's new tokens the slots its block table gives their positions, and
+ * no sequence's new slots lie inside another sequence's context. Otherwise the two calls run. Outputs and caches are
+ * then identical to the two calls; num_tokens = the rows of key / value and slot_mapping; plan as vox_prefill_attn's,
+ * except that a REUSE call needs a record made by this function (records hold the new tokens' slots). */
+int vox_prefill_attn_store_paged(const void* q, int64_t q_row_stride, const void* key, const void* value,
+                                 int64_t key_row_stride, int64_t value_row_stride, const int32_t* slot_mapping,
+                                 int64_t num_tokens, void* k_cache, void* v_cache, int64_t num_blocks, int block_size,
+                                 const int32_t* block_tables, int64_t bt_stride, int max_blocks,
+                                 const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch, int max_seqlen_q,
+                                 int num_heads, int num_kv_heads, int head_dim, float softmax_scale, int causal,
+                                 void* out, int64_t out_row_stride, int plan, void* workspace, size_t workspace_bytes,
+                                 void* stream);
 
 /* vox_prefill_attn with the int8 output epilogue the W8A8 o_proj consumes. Replaces the quant=True modes of the
  * Triton paged_prefill_attention, short_causal_attention and short_attention (reference:

@@ -311,3 +311,27 @@ def test_flash_attn_entry_points_take_flash_attn_2_8_3_positional_order():
 def test_python_errors_carry_the_library_message():
     with pytest.raises(ValueError, match="head_dim"):
         _lib.check(_decode(d=64), "decode_attn")
+
+
+def test_prefill_store_paged_rejects_bad_arguments_before_launching():
+    """The paged prefill with the store riding in it (a mixed step's call) checks every argument of both parts,
+    the workspace and the plan mode included, before it launches anything; nothing to attend and nothing to store is
+    a no-op."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    # q, q stride, key, value, key/value strides, slots, num_tokens, k/v cache, num_blocks, block_size, table, table
+    # stride, max_blocks, cu_q, cu_k, batch, max_seqlen_q, H, HK, D, scale, causal, out, out stride, plan, workspace,
+    # its bytes, stream (fake pointers: never passed unmodified)
+    args = [p, 2560, p, p, 2560, 2560, p, 100, p, p, 512, 256, p, 8, 8, p, p, 2, 64, 16, 2, 128, 0.088, 1, p, 2048, 0,
+            p, 1 << 30, None]
+    for i, val, msg in [(21, 64, "head_dim"), (2, None, "null"), (6, None, "null"), (12, None, "null"),
+                        (15, None, "null"), (4, 200, "row strides"), (10, 0, "empty cache"), (17, -1, "negative"),
+                        (7, -5, "negative"), (24, None, "null out"), (25, 100, "out row stride"), (20, 3, "multiple"),
+                        (13, 4, "block table"), (26, 5, "plan mode"), (28, 16, "workspace")]:
+        bad = list(args)
+        bad[i] = val
+        assert lib.vox_prefill_attn_store_paged(*bad) == _lib.VOX_EINVAL, (i, val)
+        assert msg in _err(), (i, val, _err())
+    empty = list(args)
+    empty[17], empty[7] = 0, 0  # no sequences, no rows
+    assert lib.vox_prefill_attn_store_paged(*empty) == _lib.VOX_OK

@@ -187,19 +187,48 @@ def test_prefill_without_prefix_stores_and_attends_over_the_step_kv_in_one_call(
     ((n0, a0, kw0),) = rec.calls
     assert n0 == "prefill_attention_store" and a0[0] is q and a0[1] is k and a0[2] is v
     assert a0[3] is attn.k_cache and a0[4] is attn.v_cache and a0[5] is slots
-    assert kw0 == dict(cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=5, softmax_scale=0.125, causal=True)
+    assert kw0 == dict(cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=5, softmax_scale=0.125, causal=True,
+                       block_table=None, plan=None)
 
 
-def test_prefill_with_block_tables_reads_the_caches(monkeypatch):
+def test_prefill_with_block_tables_stores_and_attends_through_the_tables_in_one_call(monkeypatch):
+    """store_kvcache then flash_attn_varlen_func over the caches through the block tables (reference
+    layers.py:332-348 with a prefix cache or a mixed step): one prefill_attention_store call with the table and the
+    step's plan key."""
+    rec = _Recorder(monkeypatch)
+    attn = Attention(16, 128, 0.125, 2)
+    attn.k_cache, attn.v_cache = torch.zeros(2, 256, 2, 128), torch.zeros(2, 256, 2, 128)
+    bt = torch.tensor([[1, 0]], dtype=torch.int32)
+    slots = torch.tensor([298, 299], dtype=torch.int32)
+    set_context(True, torch.tensor([0, 2], dtype=torch.int32), torch.tensor([0, 300], dtype=torch.int32), 2, 300,
+                slots, None, bt)
+    q, k, v = torch.zeros(2, 16, 128), torch.zeros(2, 2, 128), torch.zeros(2, 2, 128)
+    assert attn(q, k, v) == "o"
+    ((n0, a0, kw0),) = rec.calls
+    assert n0 == "prefill_attention_store" and a0[0] is q and a0[1] is k and a0[2] is v and a0[5] is slots
+    assert a0[3] is attn.k_cache and a0[4] is attn.v_cache and kw0["block_table"] is bt
+    assert kw0["plan"] is not None and kw0["max_seqlen_q"] == 2
+
+
+def test_prefill_rows_the_riding_store_cannot_take_store_then_attend(monkeypatch):
+    """Key / value rows whose heads are not contiguous, or a slot_mapping that is not one slot per row, take
+    store_kvcache then flash_attn_varlen_func over the caches."""
     rec = _Recorder(monkeypatch)
     attn = Attention(16, 128, 0.125, 2)
     attn.k_cache, attn.v_cache = torch.zeros(2, 256, 2, 128), torch.zeros(2, 256, 2, 128)
     bt = torch.tensor([[1, 0]], dtype=torch.int32)
     set_context(True, torch.tensor([0, 2], dtype=torch.int32), torch.tensor([0, 300], dtype=torch.int32), 2, 300,
-                torch.tensor([298, 299], dtype=torch.int32), None, bt)
+                torch.tensor([298, 299, 300], dtype=torch.int32), None, bt)
     attn(torch.zeros(2, 16, 128), torch.zeros(2, 2, 128), torch.zeros(2, 2, 128))
+    assert [c[0] for c in rec.calls] == ["store_kvcache", "flash_attn_varlen_func"]
     _, a1, kw1 = rec.calls[1]
     assert a1[1] is attn.k_cache and a1[2] is attn.v_cache and kw1["block_table"] is bt
+    rec.calls.clear()
+    set_context(True, torch.tensor([0, 2], dtype=torch.int32), torch.tensor([0, 300], dtype=torch.int32), 2, 300,
+                torch.tensor([298, 299], dtype=torch.int32), None, bt)
+    k = torch.zeros(2, 128, 2).transpose(1, 2)  # heads 1 element apart
+    attn(torch.zeros(2, 16, 128), k, k)
+    assert [c[0] for c in rec.calls] == ["store_kvcache", "flash_attn_varlen_func"]
 
 
 def test_warmup_prefill_without_caches_skips_the_store(monkeypatch):

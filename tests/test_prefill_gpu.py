@@ -464,10 +464,10 @@ def test_varlen_one_query_rows_run_on_the_decode_kernels():
 
 
 def test_mixed_step_captured_in_a_hip_graph_replays_like_eager():
-    """A mixed prefill + decode varlen call runs on the caller's stream: the persistent prefill grid over the
-    multi-query rows, then the decode kernel (and its merge kernel) over the one-query rows. Captured in a HIP graph and
-    replayed four times, with eager calls on other inputs between the replays, every replay equals the eager result
-    bit for bit, which is within tolerance of the oracle."""
+    """A mixed prefill + decode varlen call runs on the caller's stream: one launch whose prefill workgroups take the
+    multi-query rows and whose decode workgroups take the one-query rows, then the decode merge kernel. Captured in a
+    HIP graph and replayed four times, with eager calls on other inputs between the replays, every replay equals the
+    eager result bit for bit, which is within tolerance of the oracle."""
     gen = torch.Generator().manual_seed(91)
     pre, dec = [300, 450, 77], [700, 130, 1500, 2, 999]
     nk, nq = pre + dec, pre + [1] * len(dec)
@@ -644,3 +644,105 @@ def test_packed_prefill_with_the_store_riding_in_it_equals_store_then_prefill(ca
     assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2), f"{case}: caches differ from store_kvcache's"
     want = ref.varlen(q.float().cpu(), _cu(lens), _cu(lens), k=k.cpu(), v=v.cpu())
     attn_close(fused, want, f"{case}: against the oracle")
+
+
+def _step_with_new_rows(gen, pre, prefix, dec, hk, block_size, misalign=0):
+    """A paged step: prefills of pre[i] new tokens over prefix[i] cached ones, and one-query decode rows over dec[i]
+    keys (the last one new); caches, tables, the step's q / k / v rows (strided as the model's qkv split; with
+    `misalign`, k and v instead contiguous rows that many elements into a buffer of their own) and the slots the
+    tables give the new tokens' positions."""
+    nq = list(pre) + [1] * len(dec)
+    nk = [a + b for a, b in zip(pre, prefix)] + list(dec)
+    pool = sum((n + block_size - 1) // block_size for n in nk) + 3
+    kc, vc, tables = paged_pool(gen, nk, pool, block_size=block_size, hk=hk)
+    T = sum(nq)
+    q, k, v = randn(gen, T, (H + 2 * hk) * D).to(DEV).split([H * D, hk * D, hk * D], dim=-1)
+    q, k, v = q.view(T, H, D), k.view(T, hk, D), v.view(T, hk, D)
+    if misalign:
+        kv = torch.empty(2 * T * hk * D + misalign, dtype=torch.bfloat16, device=DEV)
+        k2, v2 = kv[misalign:].view(2, T, hk, D)
+        k2.copy_(k)
+        v2.copy_(v)
+        k, v = k2, v2
+    slots = torch.tensor([ref.slot_of(tables[b].tolist(), j, block_size)
+                          for b in range(len(nk)) for j in range(nk[b] - nq[b], nk[b])], dtype=torch.int32)
+    return nq, nk, kc, vc, tables, q, k, v, slots
+
+
+@pytest.mark.parametrize("case", ["config5", "prefixes", "one_kv_head", "unaligned_rows", "dense", "planned"])
+def test_paged_prefill_with_the_store_riding_in_it_equals_store_then_prefill(case):
+    """prefill_attention_store with a block table (a mixed step's call: the launch reads each sequence's new keys
+    from the rows, the merge kernel writes the caches) against store_kvcache then flash_attn_varlen_func over the
+    caches: outputs and both caches bit-identical, the outputs within tolerance of the oracle over the stored caches.
+    Cases: config 5 (6 prefills of U[300, 600] new tokens, 120 decode rows over U[128, 1800] keys, 256-token blocks);
+    prefills over cached prefixes of 1-300 tokens, so that tiles straddle the first new key at every offset inside a
+    16-key piece and at piece edges (64-token blocks), beside decode rows; one kv head; key / value rows that are not
+    16-byte aligned (the two calls); a dense prefill, where the one-query rows stay on the prefill kernel (the two
+    calls); the config 5 step over three layers with a plan (record, reuse, reuse)."""
+    from voxcpm2_arabic_dialects_turbo_amd.ops import prefill_attention_store
+
+    gen = torch.Generator().manual_seed(97)
+    hk = 1 if case == "one_kv_head" else HK
+    if case in ("config5", "planned", "unaligned_rows", "one_kv_head"):
+        pre, prefix, dec, bs = uniform_lens(gen, 6, 300, 600), [0] * 6, uniform_lens(gen, 120, 128, 1800), BLOCK
+    elif case == "prefixes":
+        prefix = [1, 15, 16, 17, 31, 48, 63, 64, 65, 100, 130, 255, 256, 300]
+        pre, dec, bs = uniform_lens(gen, len(prefix), 2, 150), uniform_lens(gen, 60, 1, 700), 64
+    else:  # dense: 12 prefills of 100-200 tokens and 4 decode rows
+        pre, prefix, dec, bs = uniform_lens(gen, 12, 100, 200), [0] * 12, uniform_lens(gen, 4, 10, 300), 64
+    nq, nk, kc, vc, tables, q, k, v, slots = _step_with_new_rows(gen, pre, prefix, dec, hk, bs,
+                                                                 misalign=4 if case == "unaligned_rows" else 0)
+    cu_q, cu_k, bt, sl = _cu(nq).to(DEV), _cu(nk).to(DEV), tables.to(DEV), slots.to(DEV)
+    kc1, vc1 = kc.to(DEV), vc.to(DEV)
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    kw = dict(cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, max_seqlen_q=max(nq), softmax_scale=SCALE, block_table=bt)
+    fused = prefill_attention_store(q, k, v, kc1, vc1, sl, **kw)
+    store_kvcache(k, v, kc2, vc2, sl)
+    two = flash_attn_varlen_func(q, kc2, vc2, cu_q, cu_k, max(nq), max(nk), softmax_scale=SCALE, causal=True,
+                                 block_table=bt)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, two), f"{case}: outputs differ from store + prefill"
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2), f"{case}: caches differ from store_kvcache's"
+    if case == "planned":
+        for i in range(3):
+            o = prefill_attention_store(q, k, v, kc1, vc1, sl, plan=("riding store plan test", 1), **kw)
+            torch.cuda.synchronize()
+            assert torch.equal(o, fused), f"layer {i} ({'record' if i == 0 else 'reuse'}) differs"
+        assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    want = ref.varlen(q.float().cpu(), _cu(nq), _cu(nk), k_cache=kc2.cpu(), v_cache=vc2.cpu(), block_tables=tables)
+    attn_close(fused, want, f"{case}: against the oracle")
+
+
+def test_mixed_step_with_the_riding_store_replays_in_a_hip_graph():
+    """Attention.forward over a mixed step with caches (the store riding in the mixed launch) captured in a HIP graph
+    and replayed three times, with eager calls on other queries between the replays: every replay equals the eager
+    output bit for bit, and the caches hold the stored rows."""
+    from voxcpm2_arabic_dialects_turbo_amd.context import reset_context, set_context
+    from voxcpm2_arabic_dialects_turbo_amd.layers import Attention
+
+    gen = torch.Generator().manual_seed(98)
+    nq, nk, kc, vc, tables, q, k, v, slots = _step_with_new_rows(gen, [200, 333], [0, 70], [900, 5, 1500, 64], HK,
+                                                                 BLOCK)
+    layer = Attention(H, D, SCALE, HK)
+    layer.k_cache, layer.v_cache = kc.to(DEV), vc.to(DEV)
+    kc_want, vc_want = layer.k_cache.clone(), layer.v_cache.clone()
+    store_kvcache(k, v, kc_want, vc_want, slots.to(DEV))
+    q2 = randn(gen, *q.shape).to(DEV)
+    try:
+        set_context(True, _cu(nq).to(DEV), _cu(nk).to(DEV), max(nq), max(nk), slots.to(DEV), None, tables.to(DEV))
+        eager = layer(q, k, v)
+        eager2 = layer(q2, k, v)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            static = layer(q, k, v)
+        for r in range(3):
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(static, eager), f"replay {r}"
+            other = layer(q2, k, v)
+            torch.cuda.synchronize()
+            assert torch.equal(other, eager2)
+        assert torch.equal(layer.k_cache, kc_want) and torch.equal(layer.v_cache, vc_want)
+    finally:
+        reset_context()

@@ -376,6 +376,46 @@ int prefill_setup(const char* fn, const void* q, int64_t q_row_stride, const voi
   a->causal = causal ? 1 : 0;
   return VOX_OK;
 }
+
+// Whether a varlen call's one-query rows can run on the split-KV decode kernels (paged keys, cu_seqlens, the
+// decode kernels' head and block shapes, an output the merge kernel can write with 16-byte stores, the workspace).
+bool varlen_decode_rows(const vox::PrefillArgs& a, const void* workspace, int num_kv_heads) {
+  return workspace && a.block_tables && a.cu_q && a.num_heads <= kMaxHeads && (num_kv_heads == 1 || num_kv_heads == 2) &&
+         a.block_size % 32 == 0 && (int64_t)a.max_blocks * a.block_size <= (1 << 30) && a.out_row_stride % 8 == 0 &&
+         ((uintptr_t)a.out & 15u) == 0;
+}
+int check_varlen_workspace(const char* fn, int batch, int plan, const void* workspace, size_t workspace_bytes) {
+  const size_t need = vox_prefill_workspace_bytes(batch);
+  if (workspace_bytes < need || !aligned16(workspace))
+    return fail(VOX_EINVAL, "%s: workspace of %zu bytes (16-byte aligned), %zu needed", fn, workspace_bytes, need);
+  if (plan != VOX_PLAN_NONE && plan != VOX_PLAN_RECORD && plan != VOX_PLAN_REUSE)
+    return fail(VOX_EINVAL, "%s: plan mode %d", fn, plan);
+  return VOX_OK;
+}
+// the decode kernels' arguments for the one-query rows of the paged varlen call a (varlen mode: rows from cu_seqlens)
+vox::DecodeArgs varlen_decode_args(const vox::PrefillArgs& a, int64_t q_row_stride, int64_t num_blocks, int num_heads,
+                                   int num_kv_heads) {
+  vox::DecodeArgs d{};
+  d.q = a.q;
+  d.q_row_stride = q_row_stride;
+  d.k_cache = a.k_cache;
+  d.v_cache = a.v_cache;
+  d.num_blocks = num_blocks;
+  d.block_size = a.block_size;
+  d.block_tables = a.block_tables;
+  d.bt_stride = a.bt_stride;
+  d.max_blocks = a.max_blocks;
+  d.batch = a.batch;
+  d.num_heads = num_heads;
+  d.group = num_heads / num_kv_heads;
+  d.scale_log2 = a.scale_log2;
+  d.grid = vox_decode_workgroups();
+  d.out = a.out;
+  d.out_row_stride = a.out_row_stride;
+  d.cu_q = a.cu_q;
+  d.cu_k = a.cu_k;
+  return d;
+}
 }  // namespace
 
 extern "C" {
@@ -404,38 +444,12 @@ int vox_prefill_attn(const void* q, int64_t q_row_stride, const void* key, const
   // One-query sequences of a paged varlen call (the decode rows of a mixed step) go to the split-KV decode kernels,
   // which spread long contexts over every CU; the prefill kernel takes the rest. Needs the workspace and the decode
   // kernels' shapes; otherwise the prefill kernel takes every row.
-  const bool decode_rows = workspace && block_tables && cu_seqlens_q && num_heads <= kMaxHeads &&
-                           (num_kv_heads == 1 || num_kv_heads == 2) && block_size % 32 == 0 &&
-                           (int64_t)max_blocks * block_size <= (1 << 30) && out_row_stride % 8 == 0 &&
-                           ((uintptr_t)out & 15u) == 0;
-  if (decode_rows) {
-    const size_t need = vox_prefill_workspace_bytes(batch);
-    if (workspace_bytes < need || !aligned16(workspace))
-      return fail(VOX_EINVAL, "prefill_attn: workspace of %zu bytes (16-byte aligned), %zu needed", workspace_bytes,
-                  need);
-    if (plan != VOX_PLAN_NONE && plan != VOX_PLAN_RECORD && plan != VOX_PLAN_REUSE)
-      return fail(VOX_EINVAL, "prefill_attn: plan mode %d", plan);
+  if (varlen_decode_rows(a, workspace, num_kv_heads)) {
+    const int sw = check_varlen_workspace("prefill_attn", batch, plan, workspace, workspace_bytes);
+    if (sw != VOX_OK) return sw;
     a.skip_single = 1;
     a.persistent = 1;  // the (q tile, sequence) grid would be mostly the decode rows' empty tiles
-    vox::DecodeArgs d{};
-    d.q = a.q;
-    d.q_row_stride = q_row_stride;
-    d.k_cache = a.k_cache;
-    d.v_cache = a.v_cache;
-    d.num_blocks = num_blocks;
-    d.block_size = block_size;
-    d.block_tables = block_tables;
-    d.bt_stride = bt_stride;
-    d.max_blocks = max_blocks;
-    d.batch = batch;
-    d.num_heads = num_heads;
-    d.group = num_heads / num_kv_heads;
-    d.scale_log2 = a.scale_log2;
-    d.grid = vox_decode_workgroups();
-    d.out = a.out;
-    d.out_row_stride = out_row_stride;
-    d.cu_q = cu_seqlens_q;
-    d.cu_k = cu_seqlens_k;
+    const vox::DecodeArgs d = varlen_decode_args(a, q_row_stride, num_blocks, num_heads, num_kv_heads);
     if (max_seqlen_q > 1 && vox::mixed_launch_fits(a, num_kv_heads)) {
       // both kinds of rows in one launch, sharing the CUs (then the merge kernel)
       const vox::DecodeArgs dw = with_workspace(d, batch, plan, workspace);
@@ -497,6 +511,83 @@ int vox_prefill_attn_store(const void* q, int64_t q_row_stride, const void* key,
   a.store_rows = num_tokens;
   a.store_num_slots = num_slots;
   return hip_status(vox::launch_prefill(a, max_seqlen_q, (hipStream_t)stream), "prefill_attn_store launch");
+}
+
+int vox_prefill_attn_store_paged(const void* q, int64_t q_row_stride, const void* key, const void* value,
+                                 int64_t key_row_stride, int64_t value_row_stride, const int32_t* slot_mapping,
+                                 int64_t num_tokens, void* k_cache, void* v_cache, int64_t num_blocks, int block_size,
+                                 const int32_t* block_tables, int64_t bt_stride, int max_blocks,
+                                 const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch, int max_seqlen_q,
+                                 int num_heads, int num_kv_heads, int head_dim, float softmax_scale, int causal,
+                                 void* out, int64_t out_row_stride, int plan, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  if (batch < 0 || max_seqlen_q < 0 || num_tokens < 0)
+    return fail(VOX_EINVAL, "prefill_attn_store_paged: negative batch, max_seqlen_q or num_tokens");
+  if (!key || !value || !k_cache || !v_cache || !slot_mapping || !block_tables || !cu_seqlens_q || !cu_seqlens_k)
+    return fail(VOX_EINVAL, "prefill_attn_store_paged: null pointer argument");
+  if (num_blocks <= 0 || block_size <= 0) return fail(VOX_EINVAL, "prefill_attn_store_paged: empty cache");
+  const int64_t row = (int64_t)num_kv_heads * head_dim;
+  if (num_kv_heads <= 0 || head_dim <= 0 || key_row_stride < row || value_row_stride < row)
+    return fail(VOX_EINVAL, "prefill_attn_store_paged: key / value row strides smaller than num_kv_heads * head_dim");
+  // every argument is checked before anything is launched
+  const bool attend = batch > 0 && max_seqlen_q > 0;
+  vox::PrefillArgs a;
+  if (attend) {
+    if (!out) return fail(VOX_EINVAL, "prefill_attn_store_paged: null out");
+    if (out_row_stride < (int64_t)num_heads * head_dim || out_row_stride % 4 || ((uintptr_t)out & 7u))
+      return fail(VOX_EINVAL, "prefill_attn_store_paged: bad out row stride or alignment");
+    const int st = prefill_setup("prefill_attn_store_paged", q, q_row_stride, key, value, key_row_stride,
+                                 value_row_stride, k_cache, v_cache, num_blocks, block_size, block_tables, bt_stride,
+                                 max_blocks, cu_seqlens_q, cu_seqlens_k, batch, max_seqlen_q, 0, 0, num_heads,
+                                 num_kv_heads, head_dim, softmax_scale, causal, &a);
+    if (st != VOX_OK) return st;
+    a.out = (uint16_t*)out;
+    a.out_row_stride = out_row_stride;
+    if (varlen_decode_rows(a, workspace, num_kv_heads)) {
+      const int sw = check_varlen_workspace("prefill_attn_store_paged", batch, plan, workspace, workspace_bytes);
+      if (sw != VOX_OK) return sw;
+    }
+  }
+  if (plan != VOX_PLAN_NONE && plan != VOX_PLAN_RECORD && plan != VOX_PLAN_REUSE)
+    return fail(VOX_EINVAL, "prefill_attn_store_paged: plan mode %d", plan);
+  // The store rides in the mixed launch: both roles read each sequence's new keys from the rows (the prefill tiles
+  // by position, the decode rows' tiles by slot) and the merge kernel's extra workgroups write the rows into the
+  // caches after every read. Else the two calls.
+  const bool vec16 = row % 8 == 0 && key_row_stride % 8 == 0 && value_row_stride % 8 == 0 && aligned16(key) &&
+                     aligned16(value) && aligned16(k_cache) && aligned16(v_cache) &&
+                     key_row_stride < (1 << 24) && value_row_stride < (1 << 24);
+  const bool fold = attend && num_tokens > 0 && max_seqlen_q > 1 && vec16 &&
+                    varlen_decode_rows(a, workspace, num_kv_heads) && vox::mixed_launch_fits(a, num_kv_heads);
+  if (!fold) {
+    const int st = vox_store_kvcache(key, value, key_row_stride, value_row_stride, k_cache, v_cache,
+                                     num_blocks * block_size, slot_mapping, num_tokens, num_kv_heads, head_dim, stream);
+    if (st != VOX_OK || !attend) return st;
+    return vox_prefill_attn(q, q_row_stride, key, value, key_row_stride, value_row_stride, k_cache, v_cache, num_blocks,
+                            block_size, block_tables, bt_stride, max_blocks, cu_seqlens_q, cu_seqlens_k, batch,
+                            max_seqlen_q, 0, 0, num_heads, num_kv_heads, head_dim, softmax_scale, causal, out,
+                            out_row_stride, plan, workspace, workspace_bytes, stream);
+  }
+  a.skip_single = 1;
+  a.persistent = 1;
+  a.k_src = (const uint16_t*)key;
+  a.v_src = (const uint16_t*)value;
+  a.k_row_stride = key_row_stride;
+  a.v_row_stride = value_row_stride;
+  a.new_from_rows = 1;
+  vox::DecodeArgs d = varlen_decode_args(a, q_row_stride, num_blocks, num_heads, num_kv_heads);
+  d.slot_mapping = slot_mapping;
+  d.new_k = (const uint16_t*)key;
+  d.new_v = (const uint16_t*)value;
+  d.new_k_stride = key_row_stride;
+  d.new_v_stride = value_row_stride;
+  d.copy_rows = num_tokens;
+  // about one batch of 16-byte copies per thread of a 256-thread workgroup (16 rows of 2 x 256 bf16), at most 256
+  const int64_t per_wg = 4 * 256 / (2 * row / 8);
+  const int64_t cw = (num_tokens + per_wg - 1) / per_wg;
+  d.copy_wgs = (int)(cw < 256 ? cw : 256);
+  const vox::DecodeArgs dw = with_workspace(d, batch, plan, workspace);
+  return hip_status(vox::launch_mixed(a, max_seqlen_q, dw, num_kv_heads, (hipStream_t)stream),
+                    "prefill_attn_store_paged mixed launch");
 }
 
 int vox_prefill_attn_int8(const void* q, int64_t q_row_stride, const void* key, const void* value,

@@ -383,7 +383,7 @@ __device__ __forceinline__ void decode_split(const DecodeArgs& p, const int g, c
       } else {
         l2 = p.context_lens[tid];
       }
-      if (store) slot_first = p.slot_mapping[tid];
+      if (store && !varlen) slot_first = p.slot_mapping[tid];  // (varlen mode finds the new token by position)
     }
     if constexpr (BTL) {
       constexpr int kPer = (kBtLds + kThreads - 1) / kThreads;  // entries per thread at most
@@ -435,7 +435,7 @@ __device__ __forceinline__ void decode_split(const DecodeArgs& p, const int g, c
       }
       if (bb < p.batch) {
         L.ctx[bb] = ctx;
-        if (store) L.snew[bb] = base == 0 ? slot_first : p.slot_mapping[bb];
+        if (store) L.snew[bb] = varlen ? -1 : base == 0 ? slot_first : p.slot_mapping[bb];
         L.row[bb] = row;
         L.start[bb] = run + before + incl - n;
       }
@@ -494,13 +494,14 @@ __device__ __forceinline__ void decode_split(const DecodeArgs& p, const int g, c
       load_tile<HK>(T, p, slot0, koff, voff);
       return;
     }
-    // store mode: the tile holds the new token when its slot lies in [slot0, slot0 + 16) (unmapped tiles are masked
-    // whatever they read)
-    const int bs = wb + k;
-    const int64_t dn = (int64_t)lane_val(w_snew, k) - slot0;
+    // store mode: the tile holds the new token when its slot lies in [slot0, slot0 + 16), or in varlen mode when it
+    // holds the sequence's last key, the position of its one query (the caller's slots are those its tables give
+    // the new tokens' positions); unmapped tiles are masked whatever they read
+    const int64_t nrow = lane_val(w_row, k);  // the sequence's row of new_k / new_v (b, or its query row)
+    const int64_t dn = varlen ? (int64_t)lane_val(w_ctx, k) - 1 - tok : (int64_t)lane_val(w_snew, k) - slot0;
     const int r_new = dn >= 0 && dn < kTile ? (int)dn : -1;
-    load_tile_new<HK>(T, p, slot0, koff, voff, r_new, p.new_k + (int64_t)bs * p.new_k_stride,
-                      p.new_v + (int64_t)bs * p.new_v_stride);
+    load_tile_new<HK>(T, p, slot0, koff, voff, r_new, p.new_k + nrow * p.new_k_stride,
+                      p.new_v + nrow * p.new_v_stride);
   };
   auto load_q = [&](u32x4 (&qv)[4], int k) {  // query row of head r16: d = kq*32 + jq*8 + [0, 8)
     const uint16_t* qb =

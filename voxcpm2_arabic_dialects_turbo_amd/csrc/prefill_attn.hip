@@ -62,7 +62,10 @@ constexpr int kFormRanked = 2;
 // Where a workgroup's keys come from (one kernel instance each, so no path's loop-carried state constrains another's
 // load waits): packed [Tk, HK, D] rows; the paged cache with block_size a multiple of 64 (a 64-key tile lies in one
 // block: one block id per tile); the paged cache with any other block size (one block id per 16-byte piece).
-enum KvSource { kPacked = 0, kPagedTiles = 1, kPagedPieces = 2 };
+enum KvSource { kPacked = 0, kPagedTiles = 1, kPagedPieces = 2, kPagedTilesNew = 3 };
+// kPagedTilesNew: paged tiles whose sequences' new keys come from the step's rows (PrefillArgs::new_from_rows; the
+// mixed launch with a riding store), an instance of its own so the other paged launches keep their registers
+constexpr bool kv_tiles(int kv) { return kv == kPagedTiles || kv == kPagedTilesNew; }
 
 // NW waves per KV group, each owning RT 16-row blocks of the 128 query rows: 4 waves x 32 rows keep the LDS reads per
 // MFMA low (the largest grids); 8 waves x 16 rows halve each wave's work per key tile, which shortens a workgroup's
@@ -118,7 +121,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
       k0 = p.cu_k[b];
       k1 = p.cu_k[b + 1];
     }
-    if constexpr (KV == kPagedTiles) {
+    if constexpr (kv_tiles(KV)) {
       bid0 = p.block_tables[(int64_t)b * p.bt_stride];
       const int col = (int)(threadIdx.x & 63);
       if (col < p.max_blocks) bt_row = p.block_tables[(int64_t)b * p.bt_stride + col];
@@ -126,6 +129,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
     nq = q1 - q0;
     nk = k1 - k0;
   }
+  const int nk_all = nk;  // the sequence's keys (its new ones the last nq)
   if (KV != kPacked) nk = min(nk, p.max_blocks * p.block_size);  // keys the block table can address
   const int G = p.group;
   const int BQ = ROWS / G;  // query tokens per workgroup
@@ -179,7 +183,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
   // and paged tiles inside one cache block (block_size a multiple of 64) go straight to LDS (the DMA path below);
   // other block sizes read each piece's block id one tile ahead (fetch_bids) and stage through registers.
   constexpr bool paged = KV != kPacked;
-  constexpr bool blk_tiles = KV == kPagedTiles;
+  constexpr bool blk_tiles = kv_tiles(KV);
   const int rs_k = paged ? HK * kD : (int)p.k_row_stride;  // elements between consecutive keys (< 2^24)
   const int rs_v = paged ? HK * kD : (int)p.v_row_stride;
   const int lrow = tid >> 4;
@@ -395,6 +399,13 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
     const int fk = lrow & 15, fv = 2 * (lrow & 7);  // rows PR i + lrow share these
     const uint32_t dk_off = (uint32_t)((lrow * rs_k + ((lc ^ fk) << 3)) * 2);
     const uint32_t dv_off = (uint32_t)((lrow * rs_v + ((lc ^ fv) << 3)) * 2);
+    // new keys from rows (paged tiles, new_from_rows): positions kn0 = nk - nq and later are the step's rows, strided
+    // as packed keys (the lane offsets of the same chunk permutation over the row strides)
+    constexpr bool fold = KV == kPagedTilesNew;
+    const int kn0 = nk_all - nq;
+    const int rsr_k = fold ? (int)p.k_row_stride : 0, rsr_v = fold ? (int)p.v_row_stride : 0;
+    const uint32_t dkr_off = (uint32_t)((lrow * rsr_k + ((lc ^ fk) << 3)) * 2);
+    const uint32_t dvr_off = (uint32_t)((lrow * rsr_v + ((lc ^ fv) << 3)) * 2);
     typedef __attribute__((address_space(3))) void lvoid;
     // Issues one tile's NP + NP DMA loads into (kd, vd); piece i of wave w fills rows PR i + 4 w .. + 3. In a tile
     // with missing keys each piece is a raw buffer load whose descriptor covers exactly the piece's real keys: keys
@@ -406,6 +417,10 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
       const char* kbc;
       const char* vbc;
       int nreal = min(kBK, nk - kv0);  // keys of this tile that exist
+      int sk = rs_k, sv = rs_v;        // elements between this tile's consecutive keys
+      uint32_t ko = dk_off, vo = dv_off;
+      uint8_t* kdw = kd + w * 1024;
+      uint8_t* vdw = vd + w * 1024;
       if constexpr (!paged) {
         kbc = reinterpret_cast<const char*>(p.k_src + (int64_t)(k0 + kv0) * p.k_row_stride + g * kD);
         vbc = reinterpret_cast<const char*>(p.v_src + (int64_t)(k0 + kv0) * p.v_row_stride + g * kD);
@@ -416,27 +431,68 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
         vbc = reinterpret_cast<const char*>(p.v_cache + row0 * rs_k + g * kD);
         if (!okb) nreal = 0;
         dma_mapped = okb;
+        if (fold && kv0 + kBK > kn0) {
+          // the step's rows from key kv0 on (row q0 + key - kn0; for a tile that straddles kn0 this base lies before
+          // the sequence's rows, where only the lanes of new keys, at kn0 and later, read)
+          const char* kbr = reinterpret_cast<const char*>(p.k_src + ((int64_t)q0 + kv0 - kn0) * p.k_row_stride + g * kD);
+          const char* vbr = reinterpret_cast<const char*>(p.v_src + ((int64_t)q0 + kv0 - kn0) * p.v_row_stride + g * kD);
+          if (kv0 >= kn0) {  // every key of the tile is new: the rows, as a packed tile
+            kbc = kbr;
+            vbc = vbr;
+            sk = rsr_k;
+            sv = rsr_v;
+            ko = dkr_off;
+            vo = dvr_off;
+            nreal = min(kBK, nk - kv0);
+            dma_mapped = true;
+          } else {
+            // old keys below kn0, new ones from it: per piece the lanes of old keys load from the cache and those of
+            // new keys from the rows (each lane fills its own LDS slot; a piece on one side takes one branch). Keys
+            // past nk read as zeros through the descriptors' ranges.
+            const int kc_end = min(kn0, nk);
+#pragma unroll
+            for (int i = 0; i < NP; ++i) {
+              const int plo = kv0 + PR * i;
+              const int nc = okb ? min(max(kc_end - plo, 0), PR) : 0;  // the piece's old real keys
+              const int nr = min(max(nk - plo, 0), PR);                 // its keys below nk (the rows' range)
+              const auto rkc = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbc + (int64_t)(PR * i) * rs_k * 2),
+                                                                 (short)0, nc * rs_k * 2, kBufferWord3);
+              const auto rvc = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vbc + (int64_t)(PR * i) * rs_v * 2),
+                                                                 (short)0, nc * rs_v * 2, kBufferWord3);
+              const auto rkr = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbr + (int64_t)(PR * i) * rsr_k * 2),
+                                                                 (short)0, nr * rsr_k * 2, kBufferWord3);
+              const auto rvr = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vbr + (int64_t)(PR * i) * rsr_v * 2),
+                                                                 (short)0, nr * rsr_v * 2, kBufferWord3);
+              if (plo + lrow < kn0) {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rkc, (lvoid*)(kdw + i * PR * 256), 16, dk_off, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rvc, (lvoid*)(vdw + i * PR * 256), 16, dv_off, 0, 0, 0);
+              } else {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rkr, (lvoid*)(kdw + i * PR * 256), 16, dkr_off, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rvr, (lvoid*)(vdw + i * PR * 256), 16, dvr_off, 0, 0, 0);
+              }
+            }
+            return;
+          }
+        }
       }
-      uint8_t* kdw = kd + w * 1024;
-      uint8_t* vdw = vd + w * 1024;
       if (nreal == kBK) {  // every key real: one descriptor per tile, the piece offset in the scalar offset
-        const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbc), (short)0, kBK * rs_k * 2, kBufferWord3);
-        const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vbc), (short)0, kBK * rs_v * 2, kBufferWord3);
+        const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbc), (short)0, kBK * sk * 2, kBufferWord3);
+        const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vbc), (short)0, kBK * sv * 2, kBufferWord3);
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lvoid*)(kdw + i * PR * 256), 16, dk_off, PR * i * rs_k * 2, 0, 0);
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lvoid*)(vdw + i * PR * 256), 16, dv_off, PR * i * rs_v * 2, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lvoid*)(kdw + i * PR * 256), 16, ko, PR * i * sk * 2, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lvoid*)(vdw + i * PR * 256), 16, vo, PR * i * sv * 2, 0, 0);
         }
       } else {
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
           const int rows = __builtin_amdgcn_readfirstlane(min(max(nreal - PR * i, 0), PR));  // real keys in the piece
-          const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbc + (int64_t)(PR * i) * rs_k * 2),
-                                                            (short)0, rows * rs_k * 2, kBufferWord3);
-          const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vbc + (int64_t)(PR * i) * rs_v * 2),
-                                                            (short)0, rows * rs_v * 2, kBufferWord3);
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lvoid*)(kdw + i * PR * 256), 16, dk_off, 0, 0, 0);
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lvoid*)(vdw + i * PR * 256), 16, dv_off, 0, 0, 0);
+          const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbc + (int64_t)(PR * i) * sk * 2),
+                                                            (short)0, rows * sk * 2, kBufferWord3);
+          const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vbc + (int64_t)(PR * i) * sv * 2),
+                                                            (short)0, rows * sv * 2, kBufferWord3);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lvoid*)(kdw + i * PR * 256), 16, ko, 0, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lvoid*)(vdw + i * PR * 256), 16, vo, 0, 0, 0);
         }
       }
     };
@@ -822,7 +878,7 @@ __device__ __forceinline__ void prefill_items(const PrefillArgs& p, const int g,
 // the workgroup's item (before it, the item's first wait also waited for the copy's stores: config 2 step 13.3 ->
 // 14.3 us), in workgroups [256, 512) of the launch order: at config 2 the rank-major grid's medium items, resident
 // from the start and done well before the heaviest chains (the grid's last 256, dispatched last, 13.9 us; here
-// 13.3 us, the time of the launch without the store).
+// 13.3 us, the time of the launch without the store). Non-temporal stores, as nothing in the step reads them back.
 __device__ __forceinline__ void store_rows(const PrefillArgs& p, int wid) {
   const int row = p.num_kv_heads * kD;  // elements of one K (or V) row
   const int pieces = row / 8;           // 16-byte pieces per row
@@ -852,7 +908,7 @@ __device__ __forceinline__ void store_rows(const PrefillArgs& p, int wid) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u)
       if (slot[u] >= 0 && slot[u] < p.store_num_slots)
-        *reinterpret_cast<u32x4*>(dst[u] + slot[u] * row) = val[u];
+        __builtin_nontemporal_store(val[u], reinterpret_cast<u32x4*>(dst[u] + slot[u] * row));
   }
 }
 
@@ -905,7 +961,7 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
 // one of each and the prefill rows' MFMA and LDS work runs beside the decode rows' memory stream instead of after it
 // (the dispatcher places workgroups [0, nd) one per CU, then the rest in the second slots: read back from HW_ID in a
 // working probe). One 4-wave workgroup shape, paged tiles (block_size a multiple of 64), at most 256 sequences.
-template <int HK>
+template <int HK, bool NEW>
 __global__ __launch_bounds__(256, 2) void mixed_kernel(PrefillArgs pa, DecodeArgs da) {
   using LB = dec::LdsBorrowed<HK>;
   static_assert(LB::kBufBytes == kTB, "the decode role borrows the prefill tile buffers");
@@ -928,8 +984,8 @@ __global__ __launch_bounds__(256, 2) void mixed_kernel(PrefillArgs pa, DecodeArg
   // the 64-row items for the same LDS (49.6 -> 44.0 us).
   __builtin_amdgcn_s_setprio(1);
   const DmaBufs<1> bufs{kt0, kt1, vt0, vt1};
-  prefill_items<false, kPagedTiles, 4, 2>(pa, (int)blockIdx.x - nd, (int)gridDim.x - nd, bufs,
-                                           item_lds(reinterpret_cast<int*>(aux), LB::kSeqCap, 4));
+  prefill_items<false, NEW ? kPagedTilesNew : kPagedTiles, 4, 2>(
+      pa, (int)blockIdx.x - nd, (int)gridDim.x - nd, bufs, item_lds(reinterpret_cast<int*>(aux), LB::kSeqCap, 4));
 }
 
 }  // namespace
@@ -965,22 +1021,31 @@ hipError_t launch_mixed(const PrefillArgs& a, int max_seqlen_q, const DecodeArgs
                         hipStream_t stream) {
   if (!mixed_launch_fits(a, num_kv_heads) || d.batch != a.batch || d.grid < 1 || max_seqlen_q <= 0)
     return hipErrorInvalidValue;
+  // a riding store: the prefill role's new keys from the rows, the decode role's by slot, the copy in the merge kernel
+  if (a.new_from_rows && (!a.k_src || !a.v_src || !d.slot_mapping || !d.new_k || !d.new_v || !d.cu_q ||
+                          d.copy_rows <= 0 || d.copy_wgs < 1))
+    return hipErrorInvalidValue;
   // the prefill workgroups: at most one per 128-row item, and one per CU (the other slot of each CU holds a decode
   // workgroup; a third of them more, waiting for free slots, measured slower: 49.6 -> 57.2 us)
   const int64_t bq = kRows / a.group;
   const int64_t items = ((int64_t)max_seqlen_q + bq - 1) / bq * a.batch * a.num_kv_heads;
   const int64_t np = items < device_cus() ? items : device_cus();
   const dim3 grid((unsigned)(d.grid + np)), block(256);
-  if (num_kv_heads == 1)
-    mixed_kernel<1><<<grid, block, 0, stream>>>(a, d);
+  if (num_kv_heads == 1 && a.new_from_rows)
+    mixed_kernel<1, true><<<grid, block, 0, stream>>>(a, d);
+  else if (num_kv_heads == 1)
+    mixed_kernel<1, false><<<grid, block, 0, stream>>>(a, d);
+  else if (a.new_from_rows)
+    mixed_kernel<2, true><<<grid, block, 0, stream>>>(a, d);
   else
-    mixed_kernel<2><<<grid, block, 0, stream>>>(a, d);
+    mixed_kernel<2, false><<<grid, block, 0, stream>>>(a, d);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return launch_decode_merge(d, stream);
 }
 
 hipError_t launch_prefill(const PrefillArgs& a0, int max_seqlen_q, hipStream_t stream) {
+  if (a0.new_from_rows) return hipErrorInvalidValue;  // (the mixed launch's form only)
   if (a0.store_rows > 0 && (a0.block_tables || a0.persistent || !a0.store_slots)) return hipErrorInvalidValue;
   if (max_seqlen_q <= 0 || a0.batch <= 0) return hipSuccess;
   PrefillArgs a = a0;

@@ -45,16 +45,22 @@ struct DecodeArgs {
   // of its table row, and its q and output row is cu_q[b]. Every other sequence is left alone: no keys, no output.
   const int32_t* cu_q;
   const int32_t* cu_k;
-  // Store mode (slot_mapping != nullptr; not with cu_q): this step's K/V row of every sequence, bf16 [B, HK, 128]
-  // with heads contiguous and rows new_*_stride elements apart, belongs at cache slot slot_mapping[b] (-1 = none).
-  // The split kernel reads that slot's token from the row instead of the cache (a tile holding the slot takes the
-  // row's K and V there), and the merge kernel writes the rows into the cache after every read: the result is that
-  // of storing first and then attending, as long as no sequence's slot lies inside another sequence's context.
+  // Store mode (slot_mapping != nullptr): this step's K/V row of every sequence, bf16 with heads contiguous and rows
+  // new_*_stride elements apart, belongs at cache slot slot_mapping[row] (-1 = none), row = b ([B, HK, 128] rows), or
+  // in varlen mode row = cu_q[b], the sequence's query row. The split kernel reads the new token from the row instead
+  // of the cache: the tile holding slot_mapping[b] takes the row's K and V there, or in varlen mode the tile holding
+  // the sequence's last key (the caller's slots being those its tables give the new tokens' positions). The cache
+  // writes come after every read: without cu_q the merge kernel writes each sequence's row; in varlen mode merge
+  // workgroups [B, B + copy_wgs) copy rows [0, copy_rows) (every row of the step, the prefill rows' too) to their
+  // slots. The result is that of storing first and then attending, as long as no sequence's new slot lies inside
+  // another sequence's context.
   const int32_t* slot_mapping;
   const uint16_t* new_k;
   const uint16_t* new_v;
   int64_t new_k_stride;
   int64_t new_v_stride;
+  int64_t copy_rows;
+  int copy_wgs;
 };
 
 struct PrefillArgs {
@@ -108,6 +114,10 @@ struct PrefillArgs {
   int64_t store_num_slots;
   int store_first;
   int store_wgs;
+  // paged keys with the step's new keys in rows (launch_mixed with a riding store): sequence b's keys at positions
+  // nk - nq and later (its nq new tokens, stored by this launch's merge kernel) come from k_src / v_src rows
+  // cu_q[b] + (position - (nk - nq)) instead of the cache; the earlier keys through the block table as usual
+  int new_from_rows;
 };
 
 struct CopyArgs {

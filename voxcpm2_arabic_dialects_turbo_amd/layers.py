@@ -47,6 +47,15 @@ def _store_rides_in_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sl
     return True
 
 
+def _store_rides_in_prefill(k: torch.Tensor, v: torch.Tensor, slot_mapping) -> bool:
+    """Whether a prefill step's KV store can ride in its attention call (prefill_attention_store): [N, HK, D] key and
+    value rows with heads contiguous and one slot per row. (The library itself takes the store and the attention as
+    two launches where its copy cannot move the rows.) Any other layout takes store_kvcache then the attention."""
+    if slot_mapping is None or k.dim() != 3 or v.shape != k.shape or slot_mapping.numel() != k.shape[0]:
+        return False
+    return all(t.stride(2) == 1 and t.stride(1) == t.shape[2] for t in (k, v))
+
+
 _PLAN_SERIAL = itertools.count(1)
 
 
@@ -95,14 +104,17 @@ class Attention(nn.Module):
                 return decode_attention(q, k_cache, v_cache, context.context_lens, context.block_tables, self.scale,
                                         key=k, value=v, slot_mapping=context.slot_mapping,
                                         plan=_plan_key(context)).unsqueeze(1)
-            if cached and context.is_prefill and context.block_tables is None and context.cu_seqlens_q is not None \
-                    and context.slot_mapping is not None:
-                # prefill over the step's own rows: the store rides in the attention launch, which reads the packed
-                # rows rather than the cache
+            if cached and context.is_prefill and context.cu_seqlens_q is not None \
+                    and _store_rides_in_prefill(k, v, context.slot_mapping):
+                # prefill: the store rides in the attention call. Over the step's own rows (no block table) the
+                # launch reads the packed rows; through the block tables (prefix cache, mixed steps) the launch reads
+                # each sequence's new keys from the rows and writes the caches after its reads
+                bt = context.block_tables
                 return prefill_attention_store(q, k, v, k_cache, v_cache, context.slot_mapping,
                                                cu_seqlens_q=context.cu_seqlens_q, cu_seqlens_k=context.cu_seqlens_k,
                                                max_seqlen_q=context.max_seqlen_q, softmax_scale=self.scale,
-                                               causal=True)
+                                               causal=True, block_table=bt,
+                                               plan=_plan_key(context) if bt is not None else None)
             if cached:
                 store_kvcache(k, v, k_cache, v_cache, context.slot_mapping)
             if context.is_prefill:

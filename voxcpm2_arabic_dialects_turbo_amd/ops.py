@@ -344,11 +344,15 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor | None, v: torch.Tensor | 
 def prefill_attention_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
                             v_cache: torch.Tensor, slot_mapping: torch.Tensor, *, cu_seqlens_q: torch.Tensor,
                             cu_seqlens_k: torch.Tensor, max_seqlen_q: int, softmax_scale: float, causal: bool = True,
-                            out: torch.Tensor | None = None) -> torch.Tensor:
-    """store_kvcache(k, v, k_cache, v_cache, slot_mapping) then the packed varlen attention over k / v, as one call
-    (vox_prefill_attn_store: the copy rides in the attention launch, which reads the packed rows, not the cache).
-    Same outputs and caches as the two calls. Reference: the prefill branch of nanovllm_voxcpm/model/layers.py:
-    326-348 without a block table."""
+                            out: torch.Tensor | None = None, block_table: torch.Tensor | None = None,
+                            plan=None) -> torch.Tensor:
+    """store_kvcache(k, v, k_cache, v_cache, slot_mapping) then the varlen attention, as one call. Without a block
+    table the attention reads the packed rows k / v (vox_prefill_attn_store: the copy rides in the attention launch).
+    With one it reads the caches through the table (vox_prefill_attn_store_paged): a mixed step's launch takes each
+    sequence's new keys from the rows and its merge kernel writes the caches; that needs slot_mapping to hold the
+    slots the table gives the new tokens' positions, as the engine's does. Same outputs and caches as the two calls.
+    ``plan``: as varlen_attention's (keys of its own, apart from varlen_attention's). Reference: the prefill branch of
+    nanovllm_voxcpm/model/layers.py:326-348."""
     T, H, D = q.shape
     N, HK, Dk = k.shape
     _require(k.stride(-1) == 1 and v.stride(-1) == 1, "key/value: last dim must be contiguous")
@@ -375,6 +379,28 @@ def prefill_attention_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k
     if out is None:
         out = torch.empty(T, H, D, dtype=q.dtype, device=dev)
     lib = _lib.load()
+    if block_table is not None:
+        _check_cuda(q, block_table)
+        num_blocks, block_size = k_cache.shape[0], k_cache.shape[1]
+        bt = block_table if (block_table.dtype == torch.int32 and block_table.stride(1) == 1) else \
+            _as_i32(block_table, "block_table")
+        if bt.dim() != 2 or bt.shape[0] < B:
+            raise ValueError("block_table must be [B, max_blocks]")
+        # the mixed launch (and with it the riding store) where varlen_attention would run the one-query rows on the
+        # decode kernels
+        ws, mode = None, _lib.PLAN_NONE
+        if T and B > 0 and (max_seqlen_q == 1 or 4 * T <= B * max_seqlen_q):
+            ws = decode_workspace(dev)
+            if plan is None:
+                plan = getattr(_SCOPE, "key", None)
+            mode = _plan_mode(dev, plan, "varlen-store", B, int(bt.shape[1]), H, HK, int(block_size))
+        _lib.check(lib.vox_prefill_attn_store_paged(
+            q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(), k.stride(0), v.stride(0), slots.data_ptr(), N,
+            k_cache.data_ptr(), v_cache.data_ptr(), num_blocks, block_size, bt.data_ptr(), bt.stride(0), bt.shape[1],
+            cu_q.data_ptr(), cu_k.data_ptr(), max(B, 0), int(max_seqlen_q) if T else 0, H, HK, D, float(softmax_scale),
+            1 if causal else 0, out.data_ptr(), out.stride(0), mode, None if ws is None else ws.data_ptr(),
+            0 if ws is None else ws.numel(), _lib.stream_handle(dev)), "prefill_attn_store_paged")
+        return out
     _lib.check(lib.vox_prefill_attn_store(q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(), k.stride(0),
                                           v.stride(0), slots.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
                                           k_cache.numel() // (HK * Dk), N, cu_q.data_ptr(), cu_k.data_ptr(), max(B, 0),
