@@ -550,15 +550,32 @@ int vox_prefill_attn_store_paged(const void* q, int64_t q_row_stride, const void
   }
   if (plan != VOX_PLAN_NONE && plan != VOX_PLAN_RECORD && plan != VOX_PLAN_REUSE)
     return fail(VOX_EINVAL, "prefill_attn_store_paged: plan mode %d", plan);
-  // The store rides in the mixed launch: both roles read each sequence's new keys from the rows (the prefill tiles
-  // by position, the decode rows' tiles by slot) and the merge kernel's extra workgroups write the rows into the
-  // caches after every read. Else the two calls.
+  // The store rides in the attention launch: in a mixed launch both roles read each sequence's new keys from the rows
+  // (by position) and the merge kernel's extra workgroups write the rows into the caches after every read. Else the
+  // two calls.
   const bool vec16 = row % 8 == 0 && key_row_stride % 8 == 0 && value_row_stride % 8 == 0 && aligned16(key) &&
                      aligned16(value) && aligned16(k_cache) && aligned16(v_cache) &&
                      key_row_stride < (1 << 24) && value_row_stride < (1 << 24);
-  const bool fold = attend && num_tokens > 0 && max_seqlen_q > 1 && vec16 &&
-                    varlen_decode_rows(a, workspace, num_kv_heads) && vox::mixed_launch_fits(a, num_kv_heads);
-  if (!fold) {
+  const bool decode_rows = attend && varlen_decode_rows(a, workspace, num_kv_heads);
+  const bool fold_mixed = attend && num_tokens > 0 && max_seqlen_q > 1 && vec16 && decode_rows &&
+                          vox::mixed_launch_fits(a, num_kv_heads);
+  // without the decode rows' workspace the prefill kernel takes every row: the store rides in its launch as in the
+  // packed form (the last workgroups copy the rows), the new keys read from the rows
+  const bool fold_plain = attend && num_tokens > 0 && vec16 && !decode_rows && block_size % 64 == 0;
+  if (fold_plain) {
+    a.k_src = (const uint16_t*)key;
+    a.v_src = (const uint16_t*)value;
+    a.k_row_stride = key_row_stride;
+    a.v_row_stride = value_row_stride;
+    a.new_from_rows = 1;
+    a.store_slots = slot_mapping;
+    a.store_k_cache = (uint16_t*)k_cache;
+    a.store_v_cache = (uint16_t*)v_cache;
+    a.store_rows = num_tokens;
+    a.store_num_slots = num_blocks * block_size;
+    return hip_status(vox::launch_prefill(a, max_seqlen_q, (hipStream_t)stream), "prefill_attn_store_paged launch");
+  }
+  if (!fold_mixed) {
     const int st = vox_store_kvcache(key, value, key_row_stride, value_row_stride, k_cache, v_cache,
                                      num_blocks * block_size, slot_mapping, num_tokens, num_kv_heads, head_dim, stream);
     if (st != VOX_OK || !attend) return st;

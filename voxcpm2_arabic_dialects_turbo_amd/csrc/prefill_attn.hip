@@ -29,6 +29,8 @@
 // halves step through the key tiles together). The epilogue multiplies the normalized fp32 o by inv_smooth, takes
 // the per-token max |.| across both halves (LDS atomic max on the float bits, all values >= 0), and writes
 // rint(o / scale) (round half to even) with scale = max(amax, 1e-6) / 127.
+#include <type_traits>
+
 #include "decode_body.h"
 #include "vox_common.h"
 #include "vox_kernels.h"
@@ -62,10 +64,12 @@ constexpr int kFormRanked = 2;
 // Where a workgroup's keys come from (one kernel instance each, so no path's loop-carried state constrains another's
 // load waits): packed [Tk, HK, D] rows; the paged cache with block_size a multiple of 64 (a 64-key tile lies in one
 // block: one block id per tile); the paged cache with any other block size (one block id per 16-byte piece).
-enum KvSource { kPacked = 0, kPagedTiles = 1, kPagedPieces = 2, kPagedTilesNew = 3 };
+enum KvSource { kPacked = 0, kPagedTiles = 1, kPagedPieces = 2, kPagedTilesNew = 3, kPagedTilesRows = 4 };
 // kPagedTilesNew: paged tiles whose sequences' new keys come from the step's rows (PrefillArgs::new_from_rows; the
-// mixed launch with a riding store), an instance of its own so the other paged launches keep their registers
-constexpr bool kv_tiles(int kv) { return kv == kPagedTiles || kv == kPagedTilesNew; }
+// mixed launch with a riding store), an instance of its own so the other paged launches keep their registers.
+// kPagedTilesRows: the same for the plain and rank-major prefill forms, whose items with no cached key (nk == nq) run
+// a tile loop of their own that reads only the rows.
+constexpr bool kv_tiles(int kv) { return kv == kPagedTiles || kv == kPagedTilesNew || kv == kPagedTilesRows; }
 
 // NW waves per KV group, each owning RT 16-row blocks of the 128 query rows: 4 waves x 32 rows keep the LDS reads per
 // MFMA low (the largest grids); 8 waves x 16 rows halve each wave's work per key tile, which shortens a workgroup's
@@ -401,7 +405,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
     const uint32_t dv_off = (uint32_t)((lrow * rs_v + ((lc ^ fv) << 3)) * 2);
     // new keys from rows (paged tiles, new_from_rows): positions kn0 = nk - nq and later are the step's rows, strided
     // as packed keys (the lane offsets of the same chunk permutation over the row strides)
-    constexpr bool fold = KV == kPagedTilesNew;
+    constexpr bool fold = KV == kPagedTilesNew || KV == kPagedTilesRows;
     const int kn0 = nk_all - nq;
     const int rsr_k = fold ? (int)p.k_row_stride : 0, rsr_v = fold ? (int)p.v_row_stride : 0;
     const uint32_t dkr_off = (uint32_t)((lrow * rsr_k + ((lc ^ fk) << 3)) * 2);
@@ -413,7 +417,11 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
     // clamped and no tile is patched. (The buffer form also keeps the compiler's LDS wait counting exact; the global form makes it wait
     // for every LDS read to finish.)
     bool dma_mapped = true;  // whether the most recently loaded tile's block is mapped
-    auto dma = [&](uint8_t* kd, uint8_t* vd, int kv0) {
+    // all_rows: a std::integral_constant, true for an item all of whose keys are new (kPagedTilesRows, nk == nq): its
+    // tiles all read the rows, with no per-tile choice of source (the per-tile choice, in the same loop, made the
+    // compiler fold the plain forms' two steps per iteration into one over swapped buffers and lose the DMA's overlap:
+    // config 2 paged 13.1 -> 17.3 us; the mixed kernel keeps the one loop, as its registers leave no room for two)
+    auto dma = [&](auto all_rows, uint8_t* kd, uint8_t* vd, int kv0) {
       const char* kbc;
       const char* vbc;
       int nreal = min(kBK, nk - kv0);  // keys of this tile that exist
@@ -431,48 +439,15 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
         vbc = reinterpret_cast<const char*>(p.v_cache + row0 * rs_k + g * kD);
         if (!okb) nreal = 0;
         dma_mapped = okb;
-        if (fold && kv0 + kBK > kn0) {
-          // the step's rows from key kv0 on (row q0 + key - kn0; for a tile that straddles kn0 this base lies before
-          // the sequence's rows, where only the lanes of new keys, at kn0 and later, read)
-          const char* kbr = reinterpret_cast<const char*>(p.k_src + ((int64_t)q0 + kv0 - kn0) * p.k_row_stride + g * kD);
-          const char* vbr = reinterpret_cast<const char*>(p.v_src + ((int64_t)q0 + kv0 - kn0) * p.v_row_stride + g * kD);
-          if (kv0 >= kn0) {  // every key of the tile is new: the rows, as a packed tile
-            kbc = kbr;
-            vbc = vbr;
-            sk = rsr_k;
-            sv = rsr_v;
-            ko = dkr_off;
-            vo = dvr_off;
-            nreal = min(kBK, nk - kv0);
-            dma_mapped = true;
-          } else {
-            // old keys below kn0, new ones from it: per piece the lanes of old keys load from the cache and those of
-            // new keys from the rows (each lane fills its own LDS slot; a piece on one side takes one branch). Keys
-            // past nk read as zeros through the descriptors' ranges.
-            const int kc_end = min(kn0, nk);
-#pragma unroll
-            for (int i = 0; i < NP; ++i) {
-              const int plo = kv0 + PR * i;
-              const int nc = okb ? min(max(kc_end - plo, 0), PR) : 0;  // the piece's old real keys
-              const int nr = min(max(nk - plo, 0), PR);                 // its keys below nk (the rows' range)
-              const auto rkc = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbc + (int64_t)(PR * i) * rs_k * 2),
-                                                                 (short)0, nc * rs_k * 2, kBufferWord3);
-              const auto rvc = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vbc + (int64_t)(PR * i) * rs_v * 2),
-                                                                 (short)0, nc * rs_v * 2, kBufferWord3);
-              const auto rkr = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbr + (int64_t)(PR * i) * rsr_k * 2),
-                                                                 (short)0, nr * rsr_k * 2, kBufferWord3);
-              const auto rvr = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vbr + (int64_t)(PR * i) * rsr_v * 2),
-                                                                 (short)0, nr * rsr_v * 2, kBufferWord3);
-              if (plo + lrow < kn0) {
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rkc, (lvoid*)(kdw + i * PR * 256), 16, dk_off, 0, 0, 0);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rvc, (lvoid*)(vdw + i * PR * 256), 16, dv_off, 0, 0, 0);
-              } else {
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rkr, (lvoid*)(kdw + i * PR * 256), 16, dkr_off, 0, 0, 0);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rvr, (lvoid*)(vdw + i * PR * 256), 16, dvr_off, 0, 0, 0);
-              }
-            }
-            return;
-          }
+        if (decltype(all_rows)::value || (fold && kv0 >= kn0)) {  // every key new: the rows, as a packed tile
+          kbc = reinterpret_cast<const char*>(p.k_src + ((int64_t)q0 + kv0 - kn0) * p.k_row_stride + g * kD);
+          vbc = reinterpret_cast<const char*>(p.v_src + ((int64_t)q0 + kv0 - kn0) * p.v_row_stride + g * kD);
+          sk = rsr_k;
+          sv = rsr_v;
+          ko = dkr_off;
+          vo = dvr_off;
+          nreal = min(kBK, nk - kv0);
+          dma_mapped = true;
         }
       }
       if (nreal == kBK) {  // every key real: one descriptor per tile, the piece offset in the scalar offset
@@ -546,13 +521,13 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
     // the MFMAs that consume them (left alone, the compiler waits for each operand right after reading it); the next
     // tile has landed by the barrier. (The DMA issued before the scores held them up behind its issue: config 2
     // 13.0 -> 12.8 us, paged 13.5 -> 12.9 us, 16 x 2048 276 -> 269 us; issued after the softmax it lands too late.)
-    auto step = [&](int kv0, const uint8_t* kc_, const uint8_t* vc_, uint8_t* kn, uint8_t* vn) {
+    auto step = [&](auto all_rows, int kv0, const uint8_t* kc_, const uint8_t* vc_, uint8_t* kn, uint8_t* vn) {
       const bool has_next = kv0 + kBK < kv_end;
       const bool mapped_here = dma_mapped;  // this tile was the last one loaded
       f32x4 sc[4][RT];
       scores_d(kc_, sc);
       if (has_next) {
-        dma(kn, vn, kv0 + kBK);
+        dma(all_rows, kn, vn, kv0 + kBK);
         fetch_bids(kv0 + 2 * kBK);
       }
       const bool masked = kv0 + kBK > nk || (p.causal && kv0 + kBK - 1 > first_pos);
@@ -591,17 +566,46 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
       __builtin_amdgcn_sched_group_barrier(0x008, 8 * RT, 1);
       __syncthreads();  // the next tile has landed (the barrier waits for this wave's DMA) and this one is free
     };
-    if (kv_end > 0) {
+    if constexpr (fold) {
+      // the tile that straddles kn0 (old keys below it, new ones from it) is read from the cache like the old tiles:
+      // first this workgroup writes that tile's new keys of its kv head there from the rows (the same bytes the
+      // launch's copy writes; every workgroup reading the tile writes them before its own read, and its stores have
+      // reached L2 before its DMA reads them back through it)
+      if (kn0 > 0 && kn0 % kBK != 0 && kn0 < min(nk, kv_end)) {
+        const int t1 = min((kn0 / kBK + 1) * kBK, nk);  // past the tile's last real key
+        const int col = kn0 / p.block_size;             // the tile's block (block_size a multiple of 64)
+        const int blk = col < 64 ? __builtin_amdgcn_readlane(bt_row, col)
+                                 : p.block_tables[(int64_t)b * p.bt_stride + col];
+        if (blk >= 0 && blk < p.num_blocks) {
+          for (int c = tid; c < (t1 - kn0) * 32; c += NT) {  // (key, K or V, 16-byte chunk)
+            const int key = kn0 + (c >> 5), which = (c >> 4) & 1, ch = c & 15;
+            const int64_t row = (int64_t)q0 + (key - kn0);
+            const uint16_t* src = (which ? p.v_src + row * p.v_row_stride : p.k_src + row * p.k_row_stride) + g * kD;
+            const int64_t slot = (int64_t)blk * p.block_size + key % p.block_size;
+            uint16_t* dst = const_cast<uint16_t*>(which ? p.v_cache : p.k_cache) + (slot * HK + g) * kD;
+            *reinterpret_cast<u32x4*>(dst + ch * 8) = ld_g16(src + ch * 8);
+          }
+        }
+        wait_vmem_all();
+        __syncthreads();
+      }
+    }
+    auto tiles = [&](auto all_rows) {
+      if (kv_end <= 0) return;
       tile_bid = bid0;
-      dma(kt0[half], vt0[half], 0);
+      dma(all_rows, kt0[half], vt0[half], 0);
       wait_vmem_all();  // the query, tile 0 and the table row
       fetch_bids(kBK);
       __syncthreads();
       for (int kv0 = 0; kv0 < kv_end; kv0 += 2 * kBK) {
-        step(kv0, kt0[half], vt0[half], kt1[half], vt1[half]);
-        if (kv0 + kBK < kv_end) step(kv0 + kBK, kt1[half], vt1[half], kt0[half], vt0[half]);
+        step(all_rows, kv0, kt0[half], vt0[half], kt1[half], vt1[half]);
+        if (kv0 + kBK < kv_end) step(all_rows, kv0 + kBK, kt1[half], vt1[half], kt0[half], vt0[half]);
       }
-    }
+    };
+    if (KV == kPagedTilesRows && kn0 <= 0)
+      tiles(std::integral_constant<bool, KV == kPagedTilesRows>{});
+    else
+      tiles(std::integral_constant<bool, false>{});
   } else {
     if (kv_end > 0) {
       fetch_bids(0);
@@ -925,7 +929,7 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
     const int n = p.batch * nz, id = blockIdx.x, r = id / n, c = (id + r) % n;
     const int qt = p.causal ? (int)gridDim.x / n - 1 - r : r;
     prefill_tile<QUANT, KV, NW, RT>(p, qt, c / nz, c % nz, bufs);
-    if constexpr (KV == kPacked && !QUANT)
+    if constexpr ((KV == kPacked || KV == kPagedTilesRows) && !QUANT)
       if (p.store_rows > 0 && id >= p.store_first && id < p.store_first + p.store_wgs) store_rows(p, id - p.store_first);
   } else if constexpr (FORM == kFormPersistent) {
     constexpr int NWV = NW * (QUANT ? 2 : 1);
@@ -945,7 +949,7 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
       if (p.causal) qt = (int)gridDim.x - 1 - qt;  // heavy query tiles first
     }
     prefill_tile<QUANT, KV, NW, RT>(p, qt, b, gz, bufs);
-    if constexpr (KV == kPacked && !QUANT) {
+    if constexpr ((KV == kPacked || KV == kPagedTilesRows) && !QUANT) {
       if (p.store_rows > 0) {
         const int id = (int)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
         if (id >= p.store_first && id < p.store_first + p.store_wgs) store_rows(p, id - p.store_first);
@@ -1005,7 +1009,12 @@ hipError_t launch_prefill_kind(const PrefillArgs& a, dim3 grid, hipStream_t stre
   const dim3 block(64 * NW * (QUANT ? a.num_kv_heads : 1));
   if (!a.block_tables)
     prefill_kernel<QUANT, kPacked, NW, RT, FORM><<<grid, block, 0, stream>>>(a);
-  else if (a.block_size % kBK == 0)
+  else if (a.block_size % kBK == 0 && a.new_from_rows) {
+    if constexpr (!QUANT && FORM != kFormPersistent)  // (the plain and rank-major bf16 forms take a riding store)
+      prefill_kernel<QUANT, kPagedTilesRows, NW, RT, FORM><<<grid, block, 0, stream>>>(a);
+    else
+      return hipErrorInvalidValue;
+  } else if (a.block_size % kBK == 0)
     prefill_kernel<QUANT, kPagedTiles, NW, RT, FORM><<<grid, block, 0, stream>>>(a);
   else
     prefill_kernel<QUANT, kPagedPieces, NW, RT, FORM><<<grid, block, 0, stream>>>(a);
@@ -1045,8 +1054,12 @@ hipError_t launch_mixed(const PrefillArgs& a, int max_seqlen_q, const DecodeArgs
 }
 
 hipError_t launch_prefill(const PrefillArgs& a0, int max_seqlen_q, hipStream_t stream) {
-  if (a0.new_from_rows) return hipErrorInvalidValue;  // (the mixed launch's form only)
-  if (a0.store_rows > 0 && (a0.block_tables || a0.persistent || !a0.store_slots)) return hipErrorInvalidValue;
+  // a riding store: packed keys, or paged tiles with the new keys from the rows (new_from_rows)
+  if (a0.new_from_rows && (!a0.block_tables || a0.block_size % kBK || a0.persistent || !a0.k_src || !a0.v_src ||
+                           a0.store_rows <= 0))
+    return hipErrorInvalidValue;
+  if (a0.store_rows > 0 && ((a0.block_tables && !a0.new_from_rows) || a0.persistent || !a0.store_slots))
+    return hipErrorInvalidValue;
   if (max_seqlen_q <= 0 || a0.batch <= 0) return hipSuccess;
   PrefillArgs a = a0;
   if (a.persistent) {
@@ -1074,8 +1087,8 @@ hipError_t launch_prefill(const PrefillArgs& a0, int max_seqlen_q, hipStream_t s
   // (config 2: 16.9 -> 16.2 us), while on short sequences the doubled tile loads cost more than that saves (44 x 46
   // tokens paged 12.8 -> 14.0 us, LocDiT 150 x 11 8.4 -> 10.0 us with the wider rule). A causal grid beyond two per
   // CU runs rank-major (heaviest q tiles first).
-  // a riding KV store (packed keys only) is copied by min(grid, 256) workgroups: [256, 512) in launch order, or the
-  // last ones of a smaller grid
+  // a riding KV store (packed keys, or paged tiles with the new keys from the rows) is copied by min(grid, 256)
+  // workgroups: [256, 512) in launch order, or the last ones of a smaller grid
   auto store_by = [&](int64_t nwg) {
     a.store_wgs = a.store_rows > 0 ? (int)(nwg < 256 ? nwg : 256) : 0;
     a.store_first = (int)(nwg - a.store_wgs < 256 ? nwg - a.store_wgs : 256);
