@@ -361,3 +361,65 @@ def test_copy_kv_block_prefix_keeps_the_reference_contract():
         copy_kv_block_prefix(kv.transpose(0, 1), [(0, 1, 3)])
     with pytest.raises(ValueError, match="GPU"):
         copy_kv_block_prefix(kv, [(0, 1, 3)])
+
+
+# --- the riding stores' slot conditions (checks.py) -------------------------------------------------------------------
+
+def _paged_step(nq, nk, bs=16, seed=3):
+    """A step whose slots are the ones its tables give (disjoint blocks per sequence)."""
+    gen = torch.Generator().manual_seed(seed)
+    width = max((n + bs - 1) // bs for n in nk)
+    perm = torch.randperm(64, generator=gen).tolist()
+    tables, slots, at = torch.full((len(nk), width), -1, dtype=torch.int32), [], 0
+    for b, n in enumerate(nk):
+        nb = (n + bs - 1) // bs
+        tables[b, :nb] = torch.tensor(perm[at:at + nb], dtype=torch.int32)
+        at += nb
+        slots += [int(tables[b, j // bs]) * bs + j % bs for j in range(n - nq[b], n)]
+    cu = lambda x: torch.tensor([0] + torch.tensor(x).cumsum(0).tolist(), dtype=torch.int32)
+    return cu(nq), cu(nk), tables, torch.tensor(slots, dtype=torch.int32)
+
+
+def test_riding_store_check_passes_the_engines_slots_and_names_each_kind_of_violation():
+    """The engine's slots (the tables' slots of each sequence's new positions, reference
+    engine/model_runner.py:880-883 and :919) pass, prefill and decode alike; a slot that is not its table's, a new
+    slot inside another sequence's context, rows missing from slot_mapping and a missing table are each reported."""
+    from voxcpm2_arabic_dialects_turbo_amd.checks import riding_store_violations
+
+    cu_q, cu_k, tables, slots = _paged_step([5, 1, 30, 1], [40, 17, 30, 3])
+    kw = dict(cu_seqlens_q=cu_q, cu_seqlens_k=cu_k)
+    assert riding_store_violations(slots, tables, 16, **kw) == []
+    lens = torch.tensor([40, 17, 30, 3], dtype=torch.int32)
+    dec = torch.tensor([int(tables[b, (n - 1) // 16]) * 16 + (n - 1) % 16 for b, n in enumerate(lens.tolist())],
+                       dtype=torch.int32)
+    assert riding_store_violations(dec, tables, 16, context_lens=lens) == []
+    bad = slots.clone()
+    bad[2] += 1  # sequence 0's third new token one slot off
+    v = riding_store_violations(bad, tables, 16, **kw)
+    assert len(v) == 1 and "sequence 0" in v[0] and "position 37" in v[0]
+    other = slots.clone()
+    other[5] = int(tables[0, 0]) * 16 + 3  # sequence 1's new token written into sequence 0's first block
+    v = riding_store_violations(other, tables, 16, **kw)
+    assert any("sequence 1" in m and "block table" in m for m in v)
+    assert any("inside sequence 0's context" in m for m in v)
+    assert "past slot_mapping" in riding_store_violations(slots[:10], tables, 16, **kw)[0]
+    assert "no block tables" in riding_store_violations(slots, None, 16, **kw)[0]
+
+
+def test_attention_forward_checks_the_riding_store_when_asked(monkeypatch):
+    """With VOX_CHECK_STORE=1 a step whose slots break the riding store's conditions raises before any kernel runs;
+    without it (the default) nothing is checked."""
+    rec = _Recorder(monkeypatch)
+    attn = Attention(16, 128, 0.125, 2)
+    attn.k_cache, attn.v_cache = torch.zeros(64, 16, 2, 128), torch.zeros(64, 16, 2, 128)
+    cu_q, cu_k, tables, slots = _paged_step([5, 1], [40, 17])
+    slots[0] = -1
+    set_context(True, cu_q, cu_k, 5, 40, slots, None, tables)
+    q, k, v = torch.zeros(6, 16, 128), torch.zeros(6, 2, 128), torch.zeros(6, 2, 128)
+    monkeypatch.setenv("VOX_CHECK_STORE", "1")
+    with pytest.raises(ValueError, match="riding KV store"):
+        attn(q, k, v)
+    assert rec.calls == []
+    monkeypatch.delenv("VOX_CHECK_STORE")
+    attn(q, k, v)
+    assert [c[0] for c in rec.calls] == ["prefill_attention_store"]

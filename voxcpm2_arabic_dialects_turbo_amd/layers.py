@@ -20,6 +20,7 @@ module can be captured into HIP graphs exactly where the reference captures its 
 from __future__ import annotations
 
 import itertools
+import os
 
 import torch
 from torch import nn
@@ -54,6 +55,22 @@ def _store_rides_in_prefill(k: torch.Tensor, v: torch.Tensor, slot_mapping) -> b
     if slot_mapping is None or k.dim() != 3 or v.shape != k.shape or slot_mapping.numel() != k.shape[0]:
         return False
     return all(t.stride(2) == 1 and t.stride(1) == t.shape[2] for t in (k, v))
+
+
+def _check_riding_store(context, block_size: int, decode: bool) -> None:
+    """With VOX_CHECK_STORE=1 in the environment: verify on the host that this step's slots are those its block tables
+    give the new tokens and that no new slot lies in another sequence's context, which the riding stores assume
+    (checks.py); raise ValueError otherwise. Off by default (it copies the context to the host and synchronizes)."""
+    if os.environ.get("VOX_CHECK_STORE") != "1" or context.block_tables is None:
+        return
+    from .checks import riding_store_violations
+
+    v = riding_store_violations(context.slot_mapping, context.block_tables, block_size,
+                                context_lens=context.context_lens if decode else None,
+                                cu_seqlens_q=None if decode else context.cu_seqlens_q,
+                                cu_seqlens_k=None if decode else context.cu_seqlens_k)
+    if v:
+        raise ValueError("riding KV store: the step's slots break its assumptions: " + "; ".join(v))
 
 
 _PLAN_SERIAL = itertools.count(1)
@@ -101,6 +118,7 @@ class Attention(nn.Module):
             if cached and not context.is_prefill and _store_rides_in_decode(q, k, v, context.slot_mapping):
                 # decode step: the store rides in the decode call (one row per sequence, each writing the slot of
                 # its own newest token)
+                _check_riding_store(context, k_cache.shape[1], decode=True)
                 return decode_attention(q, k_cache, v_cache, context.context_lens, context.block_tables, self.scale,
                                         key=k, value=v, slot_mapping=context.slot_mapping,
                                         plan=_plan_key(context)).unsqueeze(1)
@@ -110,6 +128,7 @@ class Attention(nn.Module):
                 # launch reads the packed rows; through the block tables (prefix cache, mixed steps) the launch reads
                 # each sequence's new keys from the rows and writes the caches after its reads
                 bt = context.block_tables
+                _check_riding_store(context, k_cache.shape[1], decode=False)
                 return prefill_attention_store(q, k, v, k_cache, v_cache, context.slot_mapping,
                                                cu_seqlens_q=context.cu_seqlens_q, cu_seqlens_k=context.cu_seqlens_k,
                                                max_seqlen_q=context.max_seqlen_q, softmax_scale=self.scale,
