@@ -48,7 +48,11 @@ def _expect(layer: Attention, q, tasks, new_tokens):
     return torch.cat(outs)
 
 
-def test_engine_loop_prefill_with_prefix_then_decode_steps():
+def test_engine_loop_prefill_with_prefix_then_decode_steps(monkeypatch):
+    """Prefill over cached prefixes (the store riding in the attention launch, tiles straddling the first new key)
+    and decode steps (the store riding in the decode call) through the runner's contexts, against the oracle over the
+    caches; VOX_CHECK_STORE=1 also has every step's slots checked against the riding stores' conditions."""
+    monkeypatch.setenv("VOX_CHECK_STORE", "1")
     gen = torch.Generator().manual_seed(60)
     model = _model(2)
     runner.allocate_kv_cache(model, num_blocks=64, block_size=BS, device=DEV)
