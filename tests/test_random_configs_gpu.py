@@ -152,3 +152,47 @@ def test_random_decode_with_the_store_configurations(seed):
         lib.vox_set_decode_workgroups(0)
     attn_close(out, want, f"seed {seed}: B={B} heads {h}/{hk} block {bs} grid {grid}")
     assert torch.equal(k1.cpu(), k_ref) and torch.equal(v1.cpu(), v_ref), f"seed {seed}: caches differ"
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_random_prefill_with_the_store_configurations(seed):
+    """Prefill calls with the step's store riding in them through the block tables (prefill_attention_store, what
+    Attention.forward runs for a prefill or mixed step with caches) against the oracle's store followed by its varlen
+    attention over the stored caches: outputs within the tolerance, caches bit-exact. Random prefixes (so the first
+    new key falls anywhere in a tile), one-query rows among the prefills (the mixed launch when the grid is sparse,
+    the plain forms otherwise), block sizes 64-512 (and 32: the two calls), head groupings 16/2 and 8/1, decode grids."""
+    from voxcpm2_arabic_dialects_turbo_amd.ops import prefill_attention_store
+
+    gen = torch.Generator().manual_seed(5000 + seed)
+    pick = lambda xs: xs[int(torch.randint(len(xs), (1,), generator=gen))]
+    h, hk = pick([(16, 2), (8, 1)])
+    bs = pick([64, 128, 256, 512, 32])
+    n_pre, n_dec = int(torch.randint(1, 8, (1,), generator=gen)), pick([0, 3, 40, 150])
+    nq = [int(torch.randint(2, 300, (1,), generator=gen)) for _ in range(n_pre)] + [1] * n_dec
+    prefix = [pick([0, 0, int(torch.randint(1, 700, (1,), generator=gen))]) for _ in range(n_pre)]
+    nk = [a + b for a, b in zip(nq[:n_pre], prefix)] + [int(torch.randint(1, 2000, (1,), generator=gen))
+                                                         for _ in range(n_dec)]
+    order = torch.randperm(len(nq), generator=gen).tolist()  # prefills and one-query rows interleaved
+    nq, nk = [nq[i] for i in order], [nk[i] for i in order]
+    kc, vc, tables = paged_pool(gen, nk, sum(-(-n // bs) for n in nk) + 2, block_size=bs, hk=hk)
+    T = sum(nq)
+    q, key, value = randn(gen, T, h, D), randn(gen, T, hk, D), randn(gen, T, hk, D)
+    slots = torch.tensor([ref.slot_of(tables[b].tolist(), j, bs) for b in range(len(nk))
+                          for j in range(nk[b] - nq[b], nk[b])], dtype=torch.int32)
+    k_ref, v_ref = kc.clone(), vc.clone()
+    ref.store_kvcache(key, value, k_ref, v_ref, slots)
+    want = ref.varlen(q.float(), _cu(nq), _cu(nk), k_cache=k_ref, v_cache=v_ref, block_tables=tables)
+    grid = pick([0, 0, 7, 300])
+    lib = _lib.load()
+    lib.vox_set_decode_workgroups(grid)
+    try:
+        k1, v1 = kc.to(DEV), vc.to(DEV)
+        out = prefill_attention_store(q.to(DEV), key.to(DEV), value.to(DEV), k1, v1, slots.to(DEV),
+                                      cu_seqlens_q=_cu(nq).to(DEV), cu_seqlens_k=_cu(nk).to(DEV),
+                                      max_seqlen_q=max(nq), softmax_scale=SCALE, block_table=tables.to(DEV))
+        torch.cuda.synchronize()
+    finally:
+        lib.vox_set_decode_workgroups(0)
+    what = f"seed {seed}: {n_pre} prefills + {n_dec} one-query rows, heads {h}/{hk}, block {bs}, grid {grid}"
+    attn_close(out, want, what)
+    assert torch.equal(k1.cpu(), k_ref) and torch.equal(v1.cpu(), v_ref), f"{what}: caches differ"
