@@ -381,6 +381,8 @@ def prefill_attention_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k
     lib = _lib.load()
     if block_table is not None:
         _check_cuda(q, block_table)
+        if k_cache.dim() != 4 or k_cache.shape[2] != HK:
+            raise ValueError("with a block table the caches must be [num_blocks, block_size, HK, head_dim]")
         num_blocks, block_size = k_cache.shape[0], k_cache.shape[1]
         bt = block_table if (block_table.dtype == torch.int32 and block_table.stride(1) == 1) else \
             _as_i32(block_table, "block_table")
