@@ -629,7 +629,40 @@ def bench_reference_shapes(dev):
 
     ms2 = _graph_ms(run_head, 20) / n2
     out["headstart_200x7"] = dict(launch_us=round(ms2 * 1e3, 2), reference_published={"fa2_a10_us": 113})
-    del qkv
+    # the same step with its KV store (one 256-token block per sequence), bf16 and int8 output: the store riding in
+    # the attention launch (prefill_attention_store; the W8A8 layer's store_kvcache + short_causal_attention pair,
+    # kernels/fused_layer.py:643-667) against the two calls
+    from voxcpm2_arabic_dialects_turbo_amd.ops import prefill_attention_store, store_kvcache
+
+    kc2 = torch.zeros(B2, BS, HK, D, dtype=torch.bfloat16, device=dev)
+    vc2 = torch.zeros_like(kc2)
+    slots2 = (torch.arange(B2, device=dev).repeat_interleave(L2) * BS
+              + torch.arange(L2, device=dev).repeat(B2)).to(torch.int32)
+    inv2 = torch.rand(H * D, generator=gq, device=dev) + 0.5
+
+    def run_head_step(quant, mode):  # mode: "riding", "two_calls" or "attention" (no store)
+        def fn():
+            for i in range(n2):
+                q, k, v = qkv[i].split([H * D, HK * D, HK * D], dim=-1)
+                q, k, v = q.view(T2, H, D), k.view(T2, HK, D), v.view(T2, HK, D)
+                kw = dict(cu_seqlens_q=cu2, cu_seqlens_k=cu2, max_seqlen_q=L2, softmax_scale=SCALE, causal=True)
+                if quant:
+                    kw.update(quant=True, inv_smooth=inv2)
+                if mode == "riding":
+                    prefill_attention_store(q, k, v, kc2, vc2, slots2, **kw)
+                else:
+                    if mode == "two_calls":
+                        store_kvcache(k, v, kc2, vc2, slots2)
+                    varlen_attention(q, k, v, **kw)
+        return fn
+
+    for quant, key in ((False, "headstart_200x7"), (True, "headstart_200x7_int8")):
+        if quant:
+            out[key] = dict(launch_us=round(_graph_ms(run_head_step(True, "attention"), 20) / n2 * 1e3, 2))
+        step = _graph_ms(run_head_step(quant, "riding"), 20) / n2
+        two = _graph_ms(run_head_step(quant, "two_calls"), 20) / n2
+        out[key].update(step_us=round(step * 1e3, 2), step_two_calls_us=round(two * 1e3, 2))
+    del qkv, kc2, vc2
     # non-causal short rows (kernels/short_attn.py:1-10, 70-90): LocDiT 11 tokens and LocEnc 5 tokens per stream,
     # one stream per sequence of the 150-sequence decode batch; bf16 and the fused int8 output
     from voxcpm2_arabic_dialects_turbo_amd.kernels.short_attn import short_attention

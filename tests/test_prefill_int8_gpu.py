@@ -353,3 +353,52 @@ def test_int8_two_pass_in_a_hip_graph_replays_like_eager():
         other = varlen_attention(q2, k, v, **kw)
         torch.cuda.synchronize()
         assert torch.equal(other[0], eager2[0]) and torch.equal(other[1], eager2[1])
+
+
+@pytest.mark.parametrize("case", ["headstart", "ranked", "two_pass", "one_kv_head", "padded_slots", "unaligned_caches"])
+def test_int8_prefill_with_the_store_riding_in_it_equals_store_then_prefill(case, monkeypatch):
+    """prefill_attention_store(quant=True) without a block table (the W8A8 layer's store_kvcache +
+    short_causal_attention pair, nanovllm_voxcpm/kernels/fused_layer.py:643-667, as one call: the copy rides in the
+    int8 launch) against store_kvcache then varlen_attention(quant=True): codes, scales and both caches bit-identical.
+    Cases: the head-start step (200 sequences of 7 tokens, the fused epilogue's plain grid); 20 x 128 tokens with no
+    two-pass workspace (the fused epilogue's rank-major grid); config-2-like lengths (the two-pass form: the copy in
+    the bf16 pass); one kv head; padding and out-of-range slots; caches that are not 16-byte aligned (the two
+    calls)."""
+    from tests._util import BLOCK
+    from voxcpm2_arabic_dialects_turbo_amd.ops import prefill_attention_store, store_kvcache
+
+    gen = torch.Generator().manual_seed(99)
+    hk = 1 if case == "one_kv_head" else HK
+    lens = {"headstart": [7] * 200, "ranked": [128] * 20}.get(case, [412, 393, 361, 205, 108, 405, 75, 74])
+    T = sum(lens)
+    kc, vc, tables = paged_pool(gen, lens, sum(-(-n // BLOCK) for n in lens) + 2, hk=hk)
+    qkv = randn(gen, T, (H + 2 * hk) * D).to(DEV)
+    q, k, v = qkv.split([H * D, hk * D, hk * D], dim=-1)
+    q, k, v = q.view(T, H, D), k.view(T, hk, D), v.view(T, hk, D)
+    slots = torch.cat([torch.tensor([ref.slot_of(tables[b].tolist(), j, BLOCK) for j in range(n)])
+                       for b, n in enumerate(lens)]).to(torch.int32)
+    if case == "padded_slots":
+        slots[::5] = -1
+        slots[2::9] = kc.shape[0] * BLOCK + 3  # past the cache
+    inv = (torch.rand(H * D, generator=gen) + 0.5).to(DEV)
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device=DEV)
+    kc1, vc1 = kc.to(DEV), vc.to(DEV)
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    if case == "unaligned_caches":
+        def shifted(c):
+            buf = torch.empty(c.numel() + 4, dtype=c.dtype, device=DEV)
+            view = buf[4:].view(c.shape)
+            view.copy_(c)
+            return view
+        kc1, vc1 = shifted(kc1), shifted(vc1)
+    kw = dict(cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=max(lens), softmax_scale=SCALE, causal=True)
+    if case == "ranked":  # the fused epilogue rather than the two passes this shape gets a workspace for
+        lib = _lib.load()
+        assert lib.vox_prefill_int8_workspace_bytes(T, len(lens), max(lens), H, hk, D, 1) > 0
+        monkeypatch.setattr(lib, "vox_prefill_int8_workspace_bytes", lambda *a: 0)
+    codes, scales = prefill_attention_store(q, k, v, kc1, vc1, slots.to(DEV), quant=True, inv_smooth=inv, **kw)
+    store_kvcache(k, v, kc2, vc2, slots.to(DEV))
+    codes2, scales2 = varlen_attention(q, k, v, quant=True, inv_smooth=inv, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(codes, codes2) and torch.equal(scales, scales2), f"{case}: int8 output differs"
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2), f"{case}: caches differ from store_kvcache's"

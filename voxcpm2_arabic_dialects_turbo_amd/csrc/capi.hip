@@ -607,6 +607,79 @@ int vox_prefill_attn_store_paged(const void* q, int64_t q_row_stride, const void
                     "prefill_attn_store_paged mixed launch");
 }
 
+}  // extern "C"
+
+namespace {
+// A KV store riding in an int8 prefill launch over packed keys (vox_prefill_attn_int8_store): rows [0, rows) of the
+// key / value rows to slot_mapping's slots
+struct RidingStore {
+  const int32_t* slot_mapping;
+  void* k_cache;
+  void* v_cache;
+  int64_t num_slots;
+  int64_t rows;
+};
+
+int prefill_int8(const char* fn, const void* q, int64_t q_row_stride, const void* key, const void* value,
+                 int64_t key_row_stride, int64_t value_row_stride, const void* k_cache, const void* v_cache,
+                 int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride, int max_blocks,
+                 const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch, int max_seqlen_q,
+                 int uniform_seqlen_q, int uniform_seqlen_k, int num_heads, int num_kv_heads, int head_dim,
+                 float softmax_scale, int causal, const float* inv_smooth, void* out_q, int64_t out_q_row_stride,
+                 float* out_scale, int64_t num_tokens, void* workspace, size_t workspace_bytes,
+                 const RidingStore* store, bool launch, hipStream_t stream) {
+  if (!out_q || !out_scale) return fail(VOX_EINVAL, "%s: null out_q or out_scale", fn);
+  if (num_kv_heads != 1 && num_kv_heads != 2)
+    return fail(VOX_EINVAL, "%s: num_kv_heads %d unsupported (1 or 2)", fn, num_kv_heads);
+  if (out_q_row_stride < (int64_t)num_heads * head_dim || out_q_row_stride % 4 || ((uintptr_t)out_q & 3u))
+    return fail(VOX_EINVAL, "%s: bad out_q row stride or alignment", fn);
+  if (((uintptr_t)out_scale & 3u) || (inv_smooth && !aligned16(inv_smooth)))
+    return fail(VOX_EINVAL, "%s: out_scale must be 4-byte and inv_smooth 16-byte aligned", fn);
+  vox::PrefillArgs a;
+  const int st = prefill_setup(fn, q, q_row_stride, key, value, key_row_stride, value_row_stride, k_cache, v_cache,
+                               num_blocks, block_size, block_tables, bt_stride, max_blocks, cu_seqlens_q,
+                               cu_seqlens_k, batch, max_seqlen_q, uniform_seqlen_q, uniform_seqlen_k, num_heads,
+                               num_kv_heads, head_dim, softmax_scale, causal, &a);
+  if (st != VOX_OK) return st;
+  if (!cu_seqlens_q && num_tokens != (int64_t)batch * uniform_seqlen_q)
+    return fail(VOX_EINVAL, "%s: num_tokens %lld != batch x uniform_seqlen_q", fn, (long long)num_tokens);
+  // rows at or past num_tokens are never read or written, whatever cu_seqlens_q (device memory the host cannot
+  // check here) says: the outputs and the two-pass scratch are sized by num_tokens
+  a.row_limit = num_tokens;
+  const size_t need = workspace ? vox_prefill_int8_workspace_bytes(num_tokens, batch, max_seqlen_q, num_heads,
+                                                                   num_kv_heads, head_dim, causal)
+                                : 0;
+  if (need && (workspace_bytes < need || !aligned16(workspace)))
+    return fail(VOX_EINVAL, "%s: workspace of %zu bytes (16-byte aligned), %zu needed", fn, workspace_bytes, need);
+  if (!launch) return VOX_OK;  // (arguments checked only)
+  if (store) {
+    a.store_slots = store->slot_mapping;
+    a.store_k_cache = (uint16_t*)store->k_cache;
+    a.store_v_cache = (uint16_t*)store->v_cache;
+    a.store_rows = store->rows;
+    a.store_num_slots = store->num_slots;
+  }
+  if (need) {
+    // two passes: the bf16 kernel into the workspace ([T, H * 128] bf16; a riding store copied in that launch), then
+    // the per-token quantization
+    a.out = (uint16_t*)workspace;
+    a.out_row_stride = (int64_t)num_heads * head_dim;
+    const int st1 = hip_status(vox::launch_prefill(a, max_seqlen_q, stream), "prefill_attn_int8 launch");
+    if (st1 != VOX_OK) return st1;
+    return hip_status(vox::launch_quantize_rows((const uint16_t*)workspace, num_tokens, num_heads * head_dim,
+                                                inv_smooth, (int8_t*)out_q, out_q_row_stride, out_scale, stream),
+                      "prefill_attn_int8 quantization launch");
+  }
+  a.inv_smooth = inv_smooth;
+  a.out_q = (int8_t*)out_q;
+  a.out_row_stride = out_q_row_stride;
+  a.out_scale = out_scale;
+  return hip_status(vox::launch_prefill_int8(a, max_seqlen_q, stream), "prefill_attn_int8 launch");
+}
+}  // namespace
+
+extern "C" {
+
 int vox_prefill_attn_int8(const void* q, int64_t q_row_stride, const void* key, const void* value,
                           int64_t key_row_stride, int64_t value_row_stride, const void* k_cache, const void* v_cache,
                           int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
@@ -618,46 +691,55 @@ int vox_prefill_attn_int8(const void* q, int64_t q_row_stride, const void* key, 
   if (batch < 0 || max_seqlen_q < 0 || num_tokens < 0)
     return fail(VOX_EINVAL, "prefill_attn_int8: negative batch, max_seqlen_q or num_tokens");
   if (batch == 0 || max_seqlen_q == 0 || num_tokens == 0) return VOX_OK;
-  if (!out_q || !out_scale) return fail(VOX_EINVAL, "prefill_attn_int8: null out_q or out_scale");
-  if (num_kv_heads != 1 && num_kv_heads != 2)
-    return fail(VOX_EINVAL, "prefill_attn_int8: num_kv_heads %d unsupported (1 or 2)", num_kv_heads);
-  if (out_q_row_stride < (int64_t)num_heads * head_dim || out_q_row_stride % 4 || ((uintptr_t)out_q & 3u))
-    return fail(VOX_EINVAL, "prefill_attn_int8: bad out_q row stride or alignment");
-  if (((uintptr_t)out_scale & 3u) || (inv_smooth && !aligned16(inv_smooth)))
-    return fail(VOX_EINVAL, "prefill_attn_int8: out_scale must be 4-byte and inv_smooth 16-byte aligned");
-  vox::PrefillArgs a;
-  const int st = prefill_setup("prefill_attn_int8", q, q_row_stride, key, value, key_row_stride, value_row_stride,
-                               k_cache, v_cache, num_blocks, block_size, block_tables, bt_stride, max_blocks,
-                               cu_seqlens_q, cu_seqlens_k, batch, max_seqlen_q, uniform_seqlen_q, uniform_seqlen_k,
-                               num_heads, num_kv_heads, head_dim, softmax_scale, causal, &a);
-  if (st != VOX_OK) return st;
-  if (!cu_seqlens_q && num_tokens != (int64_t)batch * uniform_seqlen_q)
-    return fail(VOX_EINVAL, "prefill_attn_int8: num_tokens %lld != batch x uniform_seqlen_q", (long long)num_tokens);
-  // rows at or past num_tokens are never read or written, whatever cu_seqlens_q (device memory the host cannot
-  // check here) says: the outputs and the two-pass scratch are sized by num_tokens
-  a.row_limit = num_tokens;
-  const size_t need = workspace ? vox_prefill_int8_workspace_bytes(num_tokens, batch, max_seqlen_q, num_heads,
-                                                                   num_kv_heads, head_dim, causal)
-                                : 0;
-  if (need) {
-    // two passes: the bf16 kernel into the workspace ([T, H * 128] bf16), then the per-token quantization
-    if (workspace_bytes < need || !aligned16(workspace))
-      return fail(VOX_EINVAL, "prefill_attn_int8: workspace of %zu bytes (16-byte aligned), %zu needed",
-                  workspace_bytes, need);
-    a.out = (uint16_t*)workspace;
-    a.out_row_stride = (int64_t)num_heads * head_dim;
-    const int st1 = hip_status(vox::launch_prefill(a, max_seqlen_q, (hipStream_t)stream), "prefill_attn_int8 launch");
-    if (st1 != VOX_OK) return st1;
-    return hip_status(vox::launch_quantize_rows((const uint16_t*)workspace, num_tokens, num_heads * head_dim,
-                                                inv_smooth, (int8_t*)out_q, out_q_row_stride, out_scale,
-                                                (hipStream_t)stream),
-                      "prefill_attn_int8 quantization launch");
+  return prefill_int8("prefill_attn_int8", q, q_row_stride, key, value, key_row_stride, value_row_stride, k_cache,
+                      v_cache, num_blocks, block_size, block_tables, bt_stride, max_blocks, cu_seqlens_q,
+                      cu_seqlens_k, batch, max_seqlen_q, uniform_seqlen_q, uniform_seqlen_k, num_heads, num_kv_heads,
+                      head_dim, softmax_scale, causal, inv_smooth, out_q, out_q_row_stride, out_scale, num_tokens,
+                      workspace, workspace_bytes, nullptr, true, (hipStream_t)stream);
+}
+
+int vox_prefill_attn_int8_store(const void* q, int64_t q_row_stride, const void* key, const void* value,
+                                int64_t key_row_stride, int64_t value_row_stride, const int32_t* slot_mapping,
+                                void* k_cache, void* v_cache, int64_t num_slots, int64_t store_rows,
+                                const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch, int max_seqlen_q,
+                                int num_heads, int num_kv_heads, int head_dim, float softmax_scale, int causal,
+                                const float* inv_smooth, void* out_q, int64_t out_q_row_stride, float* out_scale,
+                                int64_t num_tokens, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "prefill_attn_int8_store";
+  if (batch < 0 || max_seqlen_q < 0 || num_tokens < 0 || store_rows < 0)
+    return fail(VOX_EINVAL, "%s: negative batch, max_seqlen_q, num_tokens or store_rows", fn);
+  if (!key || !value || !k_cache || !v_cache || !slot_mapping || !cu_seqlens_q || !cu_seqlens_k)
+    return fail(VOX_EINVAL, "%s: null pointer argument", fn);
+  if (num_slots <= 0) return fail(VOX_EINVAL, "%s: empty cache", fn);
+  const int64_t row = (int64_t)num_kv_heads * head_dim;
+  if (num_kv_heads <= 0 || head_dim <= 0 || key_row_stride < row || value_row_stride < row)
+    return fail(VOX_EINVAL, "%s: key / value row strides smaller than num_kv_heads * head_dim", fn);
+  // every argument is checked before anything is launched
+  const bool attend = batch > 0 && max_seqlen_q > 0 && num_tokens > 0;
+  if (attend) {
+    const int st = prefill_int8(fn, q, q_row_stride, key, value, key_row_stride, value_row_stride, nullptr, nullptr,
+                                0, 0, nullptr, 0, 0, cu_seqlens_q, cu_seqlens_k, batch, max_seqlen_q, 0, 0, num_heads,
+                                num_kv_heads, head_dim, softmax_scale, causal, inv_smooth, out_q, out_q_row_stride,
+                                out_scale, num_tokens, workspace, workspace_bytes, nullptr, false, nullptr);
+    if (st != VOX_OK) return st;
   }
-  a.inv_smooth = inv_smooth;
-  a.out_q = (int8_t*)out_q;
-  a.out_row_stride = out_q_row_stride;
-  a.out_scale = out_scale;
-  return hip_status(vox::launch_prefill_int8(a, max_seqlen_q, (hipStream_t)stream), "prefill_attn_int8 launch");
+  const bool vec16 = row % 8 == 0 && key_row_stride % 8 == 0 && value_row_stride % 8 == 0 && aligned16(key) &&
+                     aligned16(value) && aligned16(k_cache) && aligned16(v_cache);
+  if (!attend || !vec16 || store_rows == 0) {
+    // no launch to ride in, nothing to store, or rows the 16-byte copy cannot move: the two calls
+    const int st = vox_store_kvcache(key, value, key_row_stride, value_row_stride, k_cache, v_cache, num_slots,
+                                     slot_mapping, store_rows, num_kv_heads, head_dim, stream);
+    if (st != VOX_OK || !attend) return st;
+    return vox_prefill_attn_int8(q, q_row_stride, key, value, key_row_stride, value_row_stride, nullptr, nullptr, 0,
+                                 0, nullptr, 0, 0, cu_seqlens_q, cu_seqlens_k, batch, max_seqlen_q, 0, 0, num_heads,
+                                 num_kv_heads, head_dim, softmax_scale, causal, inv_smooth, out_q, out_q_row_stride,
+                                 out_scale, num_tokens, workspace, workspace_bytes, stream);
+  }
+  const RidingStore rs{slot_mapping, k_cache, v_cache, num_slots, store_rows};
+  return prefill_int8(fn, q, q_row_stride, key, value, key_row_stride, value_row_stride, nullptr, nullptr, 0, 0,
+                      nullptr, 0, 0, cu_seqlens_q, cu_seqlens_k, batch, max_seqlen_q, 0, 0, num_heads, num_kv_heads,
+                      head_dim, softmax_scale, causal, inv_smooth, out_q, out_q_row_stride, out_scale, num_tokens,
+                      workspace, workspace_bytes, &rs, true, (hipStream_t)stream);
 }
 
 size_t vox_prefill_int8_workspace_bytes(int64_t num_tokens, int batch, int max_seqlen_q, int num_heads,

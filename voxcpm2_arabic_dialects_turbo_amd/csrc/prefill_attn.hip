@@ -929,7 +929,7 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
     const int n = p.batch * nz, id = blockIdx.x, r = id / n, c = (id + r) % n;
     const int qt = p.causal ? (int)gridDim.x / n - 1 - r : r;
     prefill_tile<QUANT, KV, NW, RT>(p, qt, c / nz, c % nz, bufs);
-    if constexpr ((KV == kPacked || KV == kPagedTilesRows) && !QUANT)
+    if constexpr (KV == kPacked || (KV == kPagedTilesRows && !QUANT))
       if (p.store_rows > 0 && id >= p.store_first && id < p.store_first + p.store_wgs) store_rows(p, id - p.store_first);
   } else if constexpr (FORM == kFormPersistent) {
     constexpr int NWV = NW * (QUANT ? 2 : 1);
@@ -949,7 +949,7 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
       if (p.causal) qt = (int)gridDim.x - 1 - qt;  // heavy query tiles first
     }
     prefill_tile<QUANT, KV, NW, RT>(p, qt, b, gz, bufs);
-    if constexpr ((KV == kPacked || KV == kPagedTilesRows) && !QUANT) {
+    if constexpr (KV == kPacked || (KV == kPagedTilesRows && !QUANT)) {
       if (p.store_rows > 0) {
         const int id = (int)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
         if (id >= p.store_first && id < p.store_first + p.store_wgs) store_rows(p, id - p.store_first);
@@ -1145,6 +1145,13 @@ hipError_t launch_prefill_int8(const PrefillArgs& a0, int max_seqlen_q, hipStrea
   PrefillArgs a = a0;
   a.xcd_order = (int64_t)q_tiles * a.batch >= kXcdOrderMinWorkgroups;
   const dim3 grid((unsigned)q_tiles, (unsigned)a.batch, 1u);
+  // a riding KV store (packed keys only) is copied by the launch's last min(grid, 256) workgroups after their items
+  if (a.store_rows > 0) {
+    if (a.block_tables || !a.store_slots) return hipErrorInvalidValue;
+    const int64_t nwg = (int64_t)q_tiles * a.batch;
+    a.store_wgs = (int)(nwg < 256 ? nwg : 256);
+    a.store_first = (int)(nwg - a.store_wgs);
+  }
   if (r16 && a.causal && grid16 > cus)  // more items than CUs: rank-major, heaviest first
     return launch_prefill_kind<true, 4, 1, kFormRanked>(a, dim3((unsigned)grid16), stream);
   if (r16) return launch_prefill_kind<true, 4, 1>(a, grid, stream);

@@ -345,13 +345,16 @@ def prefill_attention_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k
                             v_cache: torch.Tensor, slot_mapping: torch.Tensor, *, cu_seqlens_q: torch.Tensor,
                             cu_seqlens_k: torch.Tensor, max_seqlen_q: int, softmax_scale: float, causal: bool = True,
                             out: torch.Tensor | None = None, block_table: torch.Tensor | None = None,
-                            plan=None) -> torch.Tensor:
+                            plan=None, quant: bool = False, inv_smooth: torch.Tensor | None = None):
     """store_kvcache(k, v, k_cache, v_cache, slot_mapping) then the varlen attention, as one call. Without a block
     table the attention reads the packed rows k / v (vox_prefill_attn_store: the copy rides in the attention launch).
     With one it reads the caches through the table (vox_prefill_attn_store_paged): a mixed step's launch takes each
     sequence's new keys from the rows and its merge kernel writes the caches; that needs slot_mapping to hold the
     slots the table gives the new tokens' positions, as the engine's does. Same outputs and caches as the two calls.
-    ``plan``: as varlen_attention's (keys of its own, apart from varlen_attention's). Reference: the prefill branch of
+    ``plan``: as varlen_attention's (keys of its own, apart from varlen_attention's). ``quant``: the int8 output of
+    varlen_attention(quant=True), (int8 o [T, H * D], fp32 scale [T]); without a block table the copy rides in that
+    launch (vox_prefill_attn_int8_store, the W8A8 layer's short-prefill pair store_kvcache + short_causal_attention,
+    nanovllm_voxcpm/kernels/fused_layer.py:643-667), with one the two calls run. Reference: the prefill branch of
     nanovllm_voxcpm/model/layers.py:326-348."""
     T, H, D = q.shape
     N, HK, Dk = k.shape
@@ -376,9 +379,33 @@ def prefill_attention_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k
     cu_q = _as_i32(cu_seqlens_q, "cu_seqlens_q")
     cu_k = _as_i32(cu_seqlens_k, "cu_seqlens_k")
     slots = _as_i32(slot_mapping.reshape(-1), "slot_mapping")
+    lib = _lib.load()
+    if quant:
+        if block_table is not None:  # the paged int8 form: the store, then the attention over the caches
+            store_kvcache(k, v, k_cache, v_cache, slot_mapping)
+            return varlen_attention(q, None, None, cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_seqlens_k,
+                                    max_seqlen_q=max_seqlen_q, softmax_scale=softmax_scale, causal=causal,
+                                    block_table=block_table, k_cache=k_cache, v_cache=v_cache, quant=True,
+                                    inv_smooth=inv_smooth)
+        out_q = torch.empty(T, H * D, dtype=torch.int8, device=dev)
+        out_scale = torch.empty(T, dtype=torch.float32, device=dev)
+        if inv_smooth is not None:
+            _check_cuda(q, inv_smooth)
+            if inv_smooth.numel() != H * D:
+                raise ValueError(f"inv_smooth must hold H * head_dim = {H * D} values")
+            inv_smooth = inv_smooth.reshape(-1).to(torch.float32).contiguous()
+        ws_bytes = lib.vox_prefill_int8_workspace_bytes(T, max(B, 0), int(max_seqlen_q), H, HK, D, 1 if causal else 0)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+        _lib.check(lib.vox_prefill_attn_int8_store(
+            q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(), k.stride(0), v.stride(0), slots.data_ptr(),
+            k_cache.data_ptr(), v_cache.data_ptr(), k_cache.numel() // (HK * Dk), N, cu_q.data_ptr(), cu_k.data_ptr(),
+            max(B, 0), int(max_seqlen_q) if T else 0, H, HK, D, float(softmax_scale), 1 if causal else 0,
+            None if inv_smooth is None else inv_smooth.data_ptr(), out_q.data_ptr(), out_q.stride(0),
+            out_scale.data_ptr(), T, None if ws is None else ws.data_ptr(), ws_bytes, _lib.stream_handle(dev)),
+            "prefill_attn_int8_store")
+        return out_q, out_scale
     if out is None:
         out = torch.empty(T, H, D, dtype=q.dtype, device=dev)
-    lib = _lib.load()
     if block_table is not None:
         _check_cuda(q, block_table)
         if k_cache.dim() != 4 or k_cache.shape[2] != HK:
