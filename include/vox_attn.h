@@ -168,15 +168,17 @@ int vox_prefill_attn_store(const void* q, int64_t q_row_stride, const void* key,
  * followed by vox_prefill_attn over the caches through block_tables (reference: the prefill branch of
  * nanovllm_voxcpm/model/layers.py:326-348 with a block table, store_kvcache then flash_attn_varlen_func over
  * k_cache / v_cache; the mixed steps of nanovllm_voxcpm/engine/scheduler.py:340 (_ride) take this branch).
- * When the call runs as one mixed launch (vox_prefill_attn's conditions: workspace, up to 256 sequences, blocks of a
- * multiple of 64 tokens, some sequence with more than one query) and the rows are 16-byte aligned with strides
- * multiples of 8 (below 2^24 elements), the store rides in it: each sequence's new keys (its last nq key positions) are
- * read from the rows key / value (row cu_seqlens_q[b] + i for the i-th) instead of the cache, and the merge kernel
- * writes every row into the caches after the reads. That equals the two calls when, as the engine's scheduler
+ * With blocks of a multiple of 64 tokens and rows 16-byte aligned with strides multiples of 8 (below 2^24 elements),
+ * the store rides in the attention launch: each sequence's new keys (its last nq key positions) are read from the
+ * rows key / value (row cu_seqlens_q[b] + i for the i-th) instead of the cache, and the rows are written into the
+ * caches after the reads: by the merge kernel when the call runs as one mixed launch (vox_prefill_attn's conditions:
+ * workspace, up to 256 sequences, some sequence with more than one query), else, when it runs on the prefill kernel
+ * alone (no workspace), by the launch's last workgroups. That equals the two calls when, as the engine's scheduler
  * guarantees, slot_mapping holds for each sequence's new tokens the slots its block table gives their positions, and
- * no sequence's new slots lie inside another sequence's context. Otherwise the two calls run. Outputs and caches are
- * then identical to the two calls; num_tokens = the rows of key / value and slot_mapping; plan as vox_prefill_attn's,
- * except that a REUSE call needs a record made by this function (records hold the new tokens' slots). */
+ * no sequence's new slots lie inside another sequence's context. Otherwise (a workspace whose call is not one mixed
+ * launch, other block sizes, other rows) the two calls run. Outputs and caches are identical to the two calls;
+ * num_tokens = the rows of key / value and slot_mapping; plan as vox_prefill_attn's, except that a REUSE call needs a
+ * record made by this function (records hold the new tokens' slots). */
 int vox_prefill_attn_store_paged(const void* q, int64_t q_row_stride, const void* key, const void* value,
                                  int64_t key_row_stride, int64_t value_row_stride, const int32_t* slot_mapping,
                                  int64_t num_tokens, void* k_cache, void* v_cache, int64_t num_blocks, int block_size,
