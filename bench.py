@@ -611,7 +611,33 @@ def bench_reference_shapes(dev):
         flops, nbytes = prefill_units([NEW] * B, [nk] * B)
         out[key] = dict(launch_us=round(ms * 1e3, 2), tflops=round(flops / (ms * 1e-3) / 1e12, 2),
                         reference_published=ref)
-    del kc, vc, qs
+    # the same steps with their KV store (the 46 new tokens at positions 50-95 of each sequence's block): the store
+    # riding in the attention launch (prefill_attention_store with the block table; int8: the W8A8 layer's
+    # store_kvcache + paged_prefill_attention pair, kernels/fused_layer.py:619-641) against the two calls
+    from voxcpm2_arabic_dialects_turbo_amd.ops import prefill_attention_store, store_kvcache
+
+    pos = torch.arange(PRE, nk, device=dev).repeat(B)
+    pslots = [(tables[i].view(-1).long().repeat_interleave(NEW) * BS + pos).to(torch.int32) for i in range(n_sets)]
+    kvr = torch.randn(n_sets, 2, B * NEW, HK, D, generator=gq, device=dev).to(torch.bfloat16)
+    inv = torch.rand(H * D, generator=gq, device=dev) + 0.5
+
+    def run_paged_step(quant, riding):
+        def fn():
+            for i in range(n_sets):
+                kw = dict(cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, max_seqlen_q=NEW, softmax_scale=SCALE, causal=True,
+                          block_table=tables[i], quant=quant, inv_smooth=inv if quant else None)
+                if riding:
+                    prefill_attention_store(qs[i], kvr[i, 0], kvr[i, 1], kc, vc, pslots[i], **kw)
+                else:
+                    store_kvcache(kvr[i, 0], kvr[i, 1], kc, vc, pslots[i])
+                    varlen_attention(qs[i], None, None, k_cache=kc, v_cache=vc, **kw)
+        return fn
+
+    for quant, key in ((False, "paged_prefill_44x46_prefix50"), (True, "paged_prefill_44x46_prefix50_int8")):
+        step = _graph_ms(run_paged_step(quant, True), 20) / n_sets
+        two = _graph_ms(run_paged_step(quant, False), 20) / n_sets
+        out[key].update(step_us=round(step * 1e3, 2), step_two_calls_us=round(two * 1e3, 2))
+    del kc, vc, qs, kvr
     # head-start step: 200 sequences x 7 tokens, packed, no prefix
     B2, L2 = 200, 7
     T2 = B2 * L2

@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define VOX_ABI_VERSION 12
+#define VOX_ABI_VERSION 13
 
 #define VOX_OK 0
 #define VOX_EINVAL 1 /* bad argument: shape, stride, alignment or null pointer (reference: the asserts of
@@ -214,18 +214,23 @@ int vox_prefill_attn_int8(const void* q, int64_t q_row_stride, const void* key, 
                           void* out_q, int64_t out_q_row_stride, float* out_scale, int64_t num_tokens,
                           void* workspace, size_t workspace_bytes, void* stream);
 
-/* A packed prefill step's KV store and its int8-output attention in one call: vox_store_kvcache(key, value,
- * key_row_stride, value_row_stride, k_cache, v_cache, num_slots, slot_mapping, store_rows, num_kv_heads, head_dim)
- * followed by vox_prefill_attn_int8 over the packed rows key / value (no block table). Replaces the store_kvcache +
- * short_causal_attention(quant=True) pair of the W8A8 layer's short-prefill path (reference:
- * nanovllm_voxcpm/kernels/fused_layer.py:643-667, the head-start step of a burst). The attention reads the packed
- * rows, not the cache, so the copy rides in its launch (the last workgroups copy the rows after their own work; in
- * the two-pass form, in the bf16 pass). Outputs and caches identical to the two calls; rows the 16-byte copy cannot
- * move take the two calls. Arguments as in those two functions (store_rows = the rows of key / value and
- * slot_mapping, num_tokens = the query rows). */
+/* A prefill step's KV store and its int8-output attention in one call: vox_store_kvcache(key, value, key_row_stride,
+ * value_row_stride, k_cache, v_cache, num_blocks * block_size, slot_mapping, store_rows, num_kv_heads, head_dim)
+ * followed by vox_prefill_attn_int8, over the packed rows key / value (block_tables NULL) or over the caches through
+ * block_tables. Replaces the W8A8 layer's store_kvcache + short_causal_attention(quant=True) pair (the head-start step
+ * of a burst) and its store_kvcache + paged_prefill_attention(quant=True) pair (eager prefix-cache steps) (reference:
+ * nanovllm_voxcpm/kernels/fused_layer.py:643-667 and :619-641). The copy rides in the int8 launch (the last
+ * workgroups copy the rows after their own work; in the two-pass form, in the bf16 pass); with block tables the launch
+ * reads each sequence's new keys (its last nq key positions) from the rows instead of the cache, which equals the two
+ * calls when, as the engine guarantees, slot_mapping holds the slots the tables give those positions and no sequence's
+ * new slots lie inside another sequence's context. Outputs and caches identical to the two calls; rows the 16-byte
+ * copy cannot move, and block sizes other than multiples of 64 with block tables, take the two calls. Arguments as in
+ * those two functions (k_cache / v_cache [num_blocks, block_size, HK, head_dim]; store_rows = the rows of key / value
+ * and slot_mapping, num_tokens = the query rows). */
 int vox_prefill_attn_int8_store(const void* q, int64_t q_row_stride, const void* key, const void* value,
                                 int64_t key_row_stride, int64_t value_row_stride, const int32_t* slot_mapping,
-                                void* k_cache, void* v_cache, int64_t num_slots, int64_t store_rows,
+                                int64_t store_rows, void* k_cache, void* v_cache, int64_t num_blocks, int block_size,
+                                const int32_t* block_tables, int64_t bt_stride, int max_blocks,
                                 const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch, int max_seqlen_q,
                                 int num_heads, int num_kv_heads, int head_dim, float softmax_scale, int causal,
                                 const float* inv_smooth, void* out_q, int64_t out_q_row_stride, float* out_scale,

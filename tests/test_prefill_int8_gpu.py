@@ -402,3 +402,47 @@ def test_int8_prefill_with_the_store_riding_in_it_equals_store_then_prefill(case
     torch.cuda.synchronize()
     assert torch.equal(codes, codes2) and torch.equal(scales, scales2), f"{case}: int8 output differs"
     assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2), f"{case}: caches differ from store_kvcache's"
+
+
+@pytest.mark.parametrize("case", ["prefix50", "two_pass", "one_kv_head", "blocks_of_32"])
+def test_paged_int8_prefill_with_the_store_riding_in_it_equals_store_then_prefill(case):
+    """prefill_attention_store(quant=True) through block tables (the W8A8 layer's store_kvcache +
+    paged_prefill_attention(quant=True) pair of its eager prefix-cache steps, nanovllm_voxcpm/kernels/fused_layer.py:
+    619-641, as one call: the launch reads each sequence's new keys from the rows and copies them) against
+    store_kvcache then varlen_attention(quant=True) over the caches: codes, scales and both caches bit-identical.
+    Cases: 44 sequences of 46 new tokens over 50 cached ones (the reference's shape; the fused epilogue, its tile that
+    straddles the first new key written to the cache by its readers); config-2-like lengths with no prefix (the
+    two-pass form); one kv head over prefixes; 32-token blocks (the two calls)."""
+    from voxcpm2_arabic_dialects_turbo_amd.ops import prefill_attention_store, store_kvcache
+
+    gen = torch.Generator().manual_seed(101)
+    hk = 1 if case == "one_kv_head" else HK
+    bs = 32 if case == "blocks_of_32" else 256
+    if case == "two_pass":
+        nq, pre = [412, 393, 361, 205, 108, 405, 75, 74], [0] * 8
+    elif case == "prefix50":
+        nq, pre = [46] * 44, [50] * 44
+    else:
+        nq, pre = [30, 77, 5, 120], [0, 13, 64, 200]
+    nk = [a + b for a, b in zip(nq, pre)]
+    T = sum(nq)
+    kc, vc, tables = paged_pool(gen, nk, sum(-(-n // bs) for n in nk) + 2, block_size=bs, hk=hk)
+    qkv = randn(gen, T, (H + 2 * hk) * D).to(DEV)
+    q, k, v = qkv.split([H * D, hk * D, hk * D], dim=-1)
+    q, k, v = q.view(T, H, D), k.view(T, hk, D), v.view(T, hk, D)
+    slots = torch.tensor([ref.slot_of(tables[b].tolist(), j, bs) for b in range(len(nk))
+                          for j in range(nk[b] - nq[b], nk[b])], dtype=torch.int32).to(DEV)
+    inv = (torch.rand(H * D, generator=gen) + 0.5).to(DEV)
+    cu_q = torch.tensor([0] + torch.tensor(nq).cumsum(0).tolist(), dtype=torch.int32, device=DEV)
+    cu_k = torch.tensor([0] + torch.tensor(nk).cumsum(0).tolist(), dtype=torch.int32, device=DEV)
+    bt = tables.to(DEV)
+    kc1, vc1 = kc.to(DEV), vc.to(DEV)
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    kw = dict(cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, max_seqlen_q=max(nq), softmax_scale=SCALE, causal=True,
+              quant=True, inv_smooth=inv)
+    codes, scales = prefill_attention_store(q, k, v, kc1, vc1, slots, block_table=bt, **kw)
+    store_kvcache(k, v, kc2, vc2, slots)
+    codes2, scales2 = varlen_attention(q, None, None, block_table=bt, k_cache=kc2, v_cache=vc2, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(codes, codes2) and torch.equal(scales, scales2), f"{case}: int8 output differs"
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2), f"{case}: caches differ from store_kvcache's"

@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must be loaded before the library: shared HIP runti
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvoxattn.so")
 
 VOX_OK, VOX_EINVAL, VOX_EHIP = 0, 1, 2
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 PLAN_NONE, PLAN_RECORD, PLAN_REUSE = 0, 1, 2
 
@@ -71,10 +71,10 @@ _SIGNATURES = {
                                             _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _i64, _i32, _c_void_p,
                                             _c_void_p, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _c_void_p, _i64,
                                             _i32, _c_void_p, _size, _c_void_p]),
-    "vox_prefill_attn_int8_store": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p,
-                                           _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32,
-                                           _f32, _i32, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _size,
-                                           _c_void_p]),
+    "vox_prefill_attn_int8_store": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _c_void_p, _i64,
+                                           _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _i64, _i32, _c_void_p,
+                                           _c_void_p, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _c_void_p,
+                                           _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _size, _c_void_p]),
     "vox_copy_kv_block_prefix": (_i32, [_c_void_p, _i64, _i64, _i32, _i64, _i32, _c_void_p, _i32, _i32, _c_void_p]),
     "vox_prefill_attn_int8": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64,
                                      _i32, _c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32,

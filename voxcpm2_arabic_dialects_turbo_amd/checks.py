@@ -1,8 +1,9 @@
 """Host-side check of what the riding KV stores assume about a step's slots (a debugging aid, not the hot path).
 
-A decode step's store riding in the decode call (vox_decode_attn_store), and a prefill or mixed step's store riding
-in its attention launch (vox_prefill_attn_store_paged), read each sequence's new keys from the step's key / value rows
-instead of the cache, and write the cache after their reads. The result equals store_kvcache followed by the
+A decode step's store riding in the decode call (vox_decode_attn_store), and a paged prefill or mixed step's store
+riding in its attention launch (vox_prefill_attn_store_paged; vox_prefill_attn_int8_store with block tables), read
+each sequence's new keys from the step's key / value rows instead of the cache, and write the cache after their
+reads. The result equals store_kvcache followed by the
 attention when
 
 1. each sequence's new tokens have the slots its block table gives their positions,

@@ -610,14 +610,15 @@ int vox_prefill_attn_store_paged(const void* q, int64_t q_row_stride, const void
 }  // extern "C"
 
 namespace {
-// A KV store riding in an int8 prefill launch over packed keys (vox_prefill_attn_int8_store): rows [0, rows) of the
-// key / value rows to slot_mapping's slots
+// A KV store riding in an int8 prefill launch (vox_prefill_attn_int8_store): rows [0, rows) of the key / value rows
+// to slot_mapping's slots
 struct RidingStore {
   const int32_t* slot_mapping;
   void* k_cache;
   void* v_cache;
   int64_t num_slots;
   int64_t rows;
+  bool paged;  // paged tiles: the launch reads each sequence's new keys from the rows
 };
 
 int prefill_int8(const char* fn, const void* q, int64_t q_row_stride, const void* key, const void* value,
@@ -653,6 +654,13 @@ int prefill_int8(const char* fn, const void* q, int64_t q_row_stride, const void
     return fail(VOX_EINVAL, "%s: workspace of %zu bytes (16-byte aligned), %zu needed", fn, workspace_bytes, need);
   if (!launch) return VOX_OK;  // (arguments checked only)
   if (store) {
+    if (store->paged) {
+      a.k_src = (const uint16_t*)key;
+      a.v_src = (const uint16_t*)value;
+      a.k_row_stride = key_row_stride;
+      a.v_row_stride = value_row_stride;
+      a.new_from_rows = 1;
+    }
     a.store_slots = store->slot_mapping;
     a.store_k_cache = (uint16_t*)store->k_cache;
     a.store_v_cache = (uint16_t*)store->v_cache;
@@ -700,7 +708,8 @@ int vox_prefill_attn_int8(const void* q, int64_t q_row_stride, const void* key, 
 
 int vox_prefill_attn_int8_store(const void* q, int64_t q_row_stride, const void* key, const void* value,
                                 int64_t key_row_stride, int64_t value_row_stride, const int32_t* slot_mapping,
-                                void* k_cache, void* v_cache, int64_t num_slots, int64_t store_rows,
+                                int64_t store_rows, void* k_cache, void* v_cache, int64_t num_blocks, int block_size,
+                                const int32_t* block_tables, int64_t bt_stride, int max_blocks,
                                 const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch, int max_seqlen_q,
                                 int num_heads, int num_kv_heads, int head_dim, float softmax_scale, int causal,
                                 const float* inv_smooth, void* out_q, int64_t out_q_row_stride, float* out_scale,
@@ -710,36 +719,44 @@ int vox_prefill_attn_int8_store(const void* q, int64_t q_row_stride, const void*
     return fail(VOX_EINVAL, "%s: negative batch, max_seqlen_q, num_tokens or store_rows", fn);
   if (!key || !value || !k_cache || !v_cache || !slot_mapping || !cu_seqlens_q || !cu_seqlens_k)
     return fail(VOX_EINVAL, "%s: null pointer argument", fn);
-  if (num_slots <= 0) return fail(VOX_EINVAL, "%s: empty cache", fn);
+  if (num_blocks <= 0 || block_size <= 0) return fail(VOX_EINVAL, "%s: empty cache", fn);
   const int64_t row = (int64_t)num_kv_heads * head_dim;
   if (num_kv_heads <= 0 || head_dim <= 0 || key_row_stride < row || value_row_stride < row)
     return fail(VOX_EINVAL, "%s: key / value row strides smaller than num_kv_heads * head_dim", fn);
   // every argument is checked before anything is launched
+  const bool paged = block_tables != nullptr;
   const bool attend = batch > 0 && max_seqlen_q > 0 && num_tokens > 0;
+  const void* kc_read = paged ? k_cache : nullptr;
+  const void* vc_read = paged ? v_cache : nullptr;
   if (attend) {
-    const int st = prefill_int8(fn, q, q_row_stride, key, value, key_row_stride, value_row_stride, nullptr, nullptr,
-                                0, 0, nullptr, 0, 0, cu_seqlens_q, cu_seqlens_k, batch, max_seqlen_q, 0, 0, num_heads,
-                                num_kv_heads, head_dim, softmax_scale, causal, inv_smooth, out_q, out_q_row_stride,
-                                out_scale, num_tokens, workspace, workspace_bytes, nullptr, false, nullptr);
+    const int st = prefill_int8(fn, q, q_row_stride, key, value, key_row_stride, value_row_stride, kc_read, vc_read,
+                                num_blocks, block_size, block_tables, bt_stride, max_blocks, cu_seqlens_q,
+                                cu_seqlens_k, batch, max_seqlen_q, 0, 0, num_heads, num_kv_heads, head_dim,
+                                softmax_scale, causal, inv_smooth, out_q, out_q_row_stride, out_scale, num_tokens,
+                                workspace, workspace_bytes, nullptr, false, nullptr);
     if (st != VOX_OK) return st;
   }
+  // the store rides in the launch over packed keys, or over paged tiles that read the new keys from the rows
   const bool vec16 = row % 8 == 0 && key_row_stride % 8 == 0 && value_row_stride % 8 == 0 && aligned16(key) &&
-                     aligned16(value) && aligned16(k_cache) && aligned16(v_cache);
-  if (!attend || !vec16 || store_rows == 0) {
-    // no launch to ride in, nothing to store, or rows the 16-byte copy cannot move: the two calls
-    const int st = vox_store_kvcache(key, value, key_row_stride, value_row_stride, k_cache, v_cache, num_slots,
-                                     slot_mapping, store_rows, num_kv_heads, head_dim, stream);
+                     aligned16(value) && aligned16(k_cache) && aligned16(v_cache) && key_row_stride < (1 << 24) &&
+                     value_row_stride < (1 << 24);
+  if (!attend || !vec16 || store_rows == 0 || (paged && block_size % 64 != 0)) {
+    // no launch to ride in, nothing to store, or rows / blocks the riding copy does not take: the two calls
+    const int st = vox_store_kvcache(key, value, key_row_stride, value_row_stride, k_cache, v_cache,
+                                     num_blocks * block_size, slot_mapping, store_rows, num_kv_heads, head_dim, stream);
     if (st != VOX_OK || !attend) return st;
-    return vox_prefill_attn_int8(q, q_row_stride, key, value, key_row_stride, value_row_stride, nullptr, nullptr, 0,
-                                 0, nullptr, 0, 0, cu_seqlens_q, cu_seqlens_k, batch, max_seqlen_q, 0, 0, num_heads,
-                                 num_kv_heads, head_dim, softmax_scale, causal, inv_smooth, out_q, out_q_row_stride,
-                                 out_scale, num_tokens, workspace, workspace_bytes, stream);
+    return vox_prefill_attn_int8(q, q_row_stride, key, value, key_row_stride, value_row_stride, kc_read, vc_read,
+                                 num_blocks, block_size, block_tables, bt_stride, max_blocks, cu_seqlens_q,
+                                 cu_seqlens_k, batch, max_seqlen_q, 0, 0, num_heads, num_kv_heads, head_dim,
+                                 softmax_scale, causal, inv_smooth, out_q, out_q_row_stride, out_scale, num_tokens,
+                                 workspace, workspace_bytes, stream);
   }
-  const RidingStore rs{slot_mapping, k_cache, v_cache, num_slots, store_rows};
-  return prefill_int8(fn, q, q_row_stride, key, value, key_row_stride, value_row_stride, nullptr, nullptr, 0, 0,
-                      nullptr, 0, 0, cu_seqlens_q, cu_seqlens_k, batch, max_seqlen_q, 0, 0, num_heads, num_kv_heads,
-                      head_dim, softmax_scale, causal, inv_smooth, out_q, out_q_row_stride, out_scale, num_tokens,
-                      workspace, workspace_bytes, &rs, true, (hipStream_t)stream);
+  const RidingStore rs{slot_mapping, k_cache, v_cache, num_blocks * block_size, store_rows, paged};
+  return prefill_int8(fn, q, q_row_stride, key, value, key_row_stride, value_row_stride, kc_read, vc_read, num_blocks,
+                      block_size, block_tables, bt_stride, max_blocks, cu_seqlens_q, cu_seqlens_k, batch, max_seqlen_q,
+                      0, 0, num_heads, num_kv_heads, head_dim, softmax_scale, causal, inv_smooth, out_q,
+                      out_q_row_stride, out_scale, num_tokens, workspace, workspace_bytes, &rs, true,
+                      (hipStream_t)stream);
 }
 
 size_t vox_prefill_int8_workspace_bytes(int64_t num_tokens, int batch, int max_seqlen_q, int num_heads,

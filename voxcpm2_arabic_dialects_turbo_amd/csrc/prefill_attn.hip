@@ -417,10 +417,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
     // clamped and no tile is patched. (The buffer form also keeps the compiler's LDS wait counting exact; the global form makes it wait
     // for every LDS read to finish.)
     bool dma_mapped = true;  // whether the most recently loaded tile's block is mapped
-    // all_rows: a std::integral_constant, true for an item all of whose keys are new (kPagedTilesRows, nk == nq): its
-    // tiles all read the rows, with no per-tile choice of source (the per-tile choice, in the same loop, made the
-    // compiler fold the plain forms' two steps per iteration into one over swapped buffers and lose the DMA's overlap:
-    // config 2 paged 13.1 -> 17.3 us; the mixed kernel keeps the one loop, as its registers leave no room for two)
+    // all_rows: a std::integral_constant, true for the tiles of new keys only (kPagedTilesRows' second loop): they
+    // read the rows. kPagedTilesNew (the mixed kernel, whose registers leave no room for a second loop) chooses the
+    // source per tile instead.
     auto dma = [&](auto all_rows, uint8_t* kd, uint8_t* vd, int kv0) {
       const char* kbc;
       const char* vbc;
@@ -439,7 +438,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
         vbc = reinterpret_cast<const char*>(p.v_cache + row0 * rs_k + g * kD);
         if (!okb) nreal = 0;
         dma_mapped = okb;
-        if (decltype(all_rows)::value || (fold && kv0 >= kn0)) {  // every key new: the rows, as a packed tile
+        if (decltype(all_rows)::value || (KV == kPagedTilesNew && kv0 >= kn0)) {  // all new: the rows, packed
           kbc = reinterpret_cast<const char*>(p.k_src + ((int64_t)q0 + kv0 - kn0) * p.k_row_stride + g * kD);
           vbc = reinterpret_cast<const char*>(p.v_src + ((int64_t)q0 + kv0 - kn0) * p.v_row_stride + g * kD);
           sk = rsr_k;
@@ -470,6 +469,42 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
           __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lvoid*)(vdw + i * PR * 256), 16, vo, 0, 0, 0);
         }
       }
+    };
+    // Tile 0 of an item whose first new key kn0 lies inside it (kPagedTilesRows, 0 < kn0 < 64): a lane whose key is
+    // old loads its 16 bytes from the cache block, the others from the rows (key kn0 = row q0; keys past nk out of the
+    // rows descriptor's range, read as zeros), two loads under complementary lane masks into the same LDS slots.
+    // An unmapped block reads as zeros and the tile takes no weight, as in the cache-only form.
+    auto dma_straddle0 = [&](uint8_t* kd, uint8_t* vd) {
+      const bool okb = bid0 >= 0 && bid0 < p.num_blocks;
+      const int64_t row0 = (int64_t)(okb ? bid0 : 0) * p.block_size;
+      const auto rkc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.k_cache + row0 * rs_k + g * kD),
+                                                         (short)0, okb ? kn0 * rs_k * 2 : 0, kBufferWord3);
+      const auto rvc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.v_cache + row0 * rs_k + g * kD),
+                                                         (short)0, okb ? kn0 * rs_v * 2 : 0, kBufferWord3);
+      const int nnew = min(nk, kBK) - kn0;  // the tile's new keys
+      const auto rkr = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(p.k_src + (int64_t)q0 * p.k_row_stride + g * kD), (short)0, nnew * rsr_k * 2,
+          kBufferWord3);
+      const auto rvr = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(p.v_src + (int64_t)q0 * p.v_row_stride + g * kD), (short)0, nnew * rsr_v * 2,
+          kBufferWord3);
+      uint8_t* kdw = kd + w * 1024;
+      uint8_t* vdw = vd + w * 1024;
+#pragma unroll
+      for (int i = 0; i < NP; ++i) {
+        if (PR * i + lrow < kn0) {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rkc, (lvoid*)(kdw + i * PR * 256), 16, dk_off, PR * i * rs_k * 2, 0,
+                                                   0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rvc, (lvoid*)(vdw + i * PR * 256), 16, dv_off, PR * i * rs_v * 2, 0,
+                                                   0);
+        } else {  // byte (key - kn0) x row stride + chunk of the rows (non-negative in these lanes)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rkr, (lvoid*)(kdw + i * PR * 256), 16,
+                                                   dkr_off + (uint32_t)((PR * i - kn0) * rsr_k * 2), 0, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rvr, (lvoid*)(vdw + i * PR * 256), 16,
+                                                   dvr_off + (uint32_t)((PR * i - kn0) * rsr_v * 2), 0, 0, 0);
+        }
+      }
+      dma_mapped = okb;
     };
     // K fragment (rows kt*16 + r16, chunk kc*4 + jq) at byte kt*4096 + (krd0 ^ (kc << 6))
     const uint32_t krd0 = (uint32_t)(r16 * 256 + ((jq ^ r16) << 4));
@@ -521,9 +556,10 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
     // the MFMAs that consume them (left alone, the compiler waits for each operand right after reading it); the next
     // tile has landed by the barrier. (The DMA issued before the scores held them up behind its issue: config 2
     // 13.0 -> 12.8 us, paged 13.5 -> 12.9 us, 16 x 2048 276 -> 269 us; issued after the softmax it lands too late.)
-    auto step = [&](auto all_rows, int kv0, const uint8_t* kc_, const uint8_t* vc_, uint8_t* kn, uint8_t* vn) {
-      const bool has_next = kv0 + kBK < kv_end;
-      const bool mapped_here = dma_mapped;  // this tile was the last one loaded
+    auto step = [&](auto all_rows, auto from0, int kv0, int seg_end, const uint8_t* kc_, const uint8_t* vc_,
+                    uint8_t* kn, uint8_t* vn) {
+      const bool has_next = kv0 + kBK < seg_end;
+      const bool mapped_here = decltype(all_rows)::value || dma_mapped;  // the last tile loaded (rows: mapped)
       f32x4 sc[4][RT];
       scores_d(kc_, sc);
       if (has_next) {
@@ -539,7 +575,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
           for (int rt = 0; rt < RT; ++rt) sc[kt][rt] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
       }
       u32x4 pb[2][RT];
-      if (kv0 == 0) {
+      if (decltype(from0)::value && kv0 == 0) {
         softmax(sc, pb, alpha);  // the accumulators are still zero: no rescale
         moved = false;
       } else {
@@ -567,45 +603,101 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& p, int qt, int b
       __syncthreads();  // the next tile has landed (the barrier waits for this wave's DMA) and this one is free
     };
     if constexpr (fold) {
-      // the tile that straddles kn0 (old keys below it, new ones from it) is read from the cache like the old tiles:
-      // first this workgroup writes that tile's new keys of its kv head there from the rows (the same bytes the
-      // launch's copy writes; every workgroup reading the tile writes them before its own read, and its stores have
-      // reached L2 before its DMA reads them back through it)
-      if (kn0 > 0 && kn0 % kBK != 0 && kn0 < min(nk, kv_end)) {
+      // a tile that straddles kn0 (old keys below it, new ones from it) past tile 0 is read from the cache like the
+      // old tiles: first this workgroup writes that tile's new keys of its kv head there from the rows (the same bytes
+      // the launch's copy writes; every workgroup reading the tile writes them before its own read). The mixed
+      // kernel waits for the stores here; the plain form's first tile (an older one) is waited for with them below,
+      // before the barrier after which any wave loads the straddling tile. (kPagedTilesRows patches a straddling
+      // tile 0 in LDS instead.)
+      const int straddle_from = KV == kPagedTilesRows ? kBK : 1;
+      if (kn0 >= straddle_from && kn0 % kBK != 0 && kn0 < min(nk, kv_end)) {
         const int t1 = min((kn0 / kBK + 1) * kBK, nk);  // past the tile's last real key
         const int col = kn0 / p.block_size;             // the tile's block (block_size a multiple of 64)
         const int blk = col < 64 ? __builtin_amdgcn_readlane(bt_row, col)
                                  : p.block_tables[(int64_t)b * p.bt_stride + col];
         if (blk >= 0 && blk < p.num_blocks) {
-          for (int c = tid; c < (t1 - kn0) * 32; c += NT) {  // (key, K or V, 16-byte chunk)
-            const int key = kn0 + (c >> 5), which = (c >> 4) & 1, ch = c & 15;
-            const int64_t row = (int64_t)q0 + (key - kn0);
-            const uint16_t* src = (which ? p.v_src + row * p.v_row_stride : p.k_src + row * p.k_row_stride) + g * kD;
-            const int64_t slot = (int64_t)blk * p.block_size + key % p.block_size;
-            uint16_t* dst = const_cast<uint16_t*>(which ? p.v_cache : p.k_cache) + (slot * HK + g) * kD;
-            *reinterpret_cast<u32x4*>(dst + ch * 8) = ld_g16(src + ch * 8);
+          // (key, K or V, 16-byte chunk): at most 63 x 32 = 8 NT, kU loads in flight before their stores (one in
+          // the mixed kernel, whose registers are spoken for)
+          constexpr int kU = KV == kPagedTilesRows ? 4 : 1;
+          const int nchunk = (t1 - kn0) * 32;
+          for (int c0 = 0; c0 < nchunk; c0 += kU * NT) {
+            u32x4 d[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+              const int c = min(c0 + u * NT + tid, nchunk - 1);
+              const int key = kn0 + (c >> 5), which = (c >> 4) & 1, ch = c & 15;
+              const int64_t row = (int64_t)q0 + (key - kn0);
+              d[u] = ld_g16((which ? p.v_src + row * p.v_row_stride : p.k_src + row * p.k_row_stride) + g * kD +
+                            ch * 8);
+            }
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+              const int c = c0 + u * NT + tid;
+              if (c < nchunk) {
+                const int key = kn0 + (c >> 5), which = (c >> 4) & 1, ch = c & 15;
+                const int64_t slot = (int64_t)blk * p.block_size + key % p.block_size;
+                uint16_t* dst = const_cast<uint16_t*>(which ? p.v_cache : p.k_cache) + (slot * HK + g) * kD;
+                *reinterpret_cast<u32x4*>(dst + ch * 8) = d[u];
+              }
+            }
           }
         }
-        wait_vmem_all();
-        __syncthreads();
+        if constexpr (KV == kPagedTilesNew) {
+          wait_vmem_all();
+          __syncthreads();
+        }
       }
     }
-    auto tiles = [&](auto all_rows) {
-      if (kv_end <= 0) return;
-      tile_bid = bid0;
-      dma(all_rows, kt0[half], vt0[half], 0);
-      wait_vmem_all();  // the query, tile 0 and the table row
-      fetch_bids(kBK);
-      __syncthreads();
-      for (int kv0 = 0; kv0 < kv_end; kv0 += 2 * kBK) {
-        step(all_rows, kv0, kt0[half], vt0[half], kt1[half], vt1[half]);
-        if (kv0 + kBK < kv_end) step(all_rows, kv0 + kBK, kt1[half], vt1[half], kt0[half], vt0[half]);
+    // the key tiles [kv_begin, kv_stop): the first one's DMA and its wait (unless `pre`: already loaded, into the
+    // second buffers), then two steps per iteration over the double buffers (a segment's last step issues no DMA).
+    // from0, pre: std::integral_constants. from0: the segment starts at key 0, whose tile takes the plain softmax;
+    // the steps of a segment that starts later know that none of theirs is the first tile.
+    auto tiles = [&](auto all_rows, auto from0, auto pre, int kv_begin, int kv_stop) {
+      uint8_t* const ka = decltype(pre)::value ? kt1[half] : kt0[half];
+      uint8_t* const va = decltype(pre)::value ? vt1[half] : vt0[half];
+      uint8_t* const kb = decltype(pre)::value ? kt0[half] : kt1[half];
+      uint8_t* const vb = decltype(pre)::value ? vt0[half] : vt1[half];
+      if constexpr (decltype(from0)::value) kv_begin = 0;
+      if (kv_stop <= kv_begin) return;
+      if constexpr (!decltype(pre)::value) {
+        if constexpr (decltype(from0)::value)
+          tile_bid = bid0;
+        else
+          fetch_bids(kv_begin);
+        dma(all_rows, ka, va, kv_begin);
+        wait_vmem_all();  // the query, the segment's first tile and the table row (and a straddling tile's copy)
+        fetch_bids(kv_begin + kBK);
+        __syncthreads();
+      }
+      for (int kv0 = kv_begin; kv0 < kv_stop; kv0 += 2 * kBK) {
+        step(all_rows, from0, kv0, kv_stop, ka, va, kb, vb);
+        if (kv0 + kBK < kv_stop) step(all_rows, from0, kv0 + kBK, kv_stop, kb, vb, ka, va);
       }
     };
-    if (KV == kPagedTilesRows && kn0 <= 0)
-      tiles(std::integral_constant<bool, KV == kPagedTilesRows>{});
-    else
-      tiles(std::integral_constant<bool, false>{});
+    using T = std::true_type;
+    using F = std::false_type;
+    if constexpr (KV == kPagedTilesRows) {
+      // the tiles holding an old key come from the cache, the rest from the rows, in loops of one source each (a
+      // per-tile choice of source inside one loop measured slower: config 2 paged 13.1 -> 17.3 us)
+      if (kn0 <= 0) {
+        tiles(T{}, T{}, F{}, 0, kv_end);
+      } else if (kn0 < kBK) {
+        // tile 0 straddles kn0: each lane's 16 bytes of it from the cache (an old key) or from the rows (a new one),
+        // and tile 1 (all new) from the rows into the second buffers, all in one round trip
+        if (kv_end > kBK) dma(T{}, kt1[half], vt1[half], kBK);
+        dma_straddle0(kt0[half], vt0[half]);
+        wait_vmem_all();
+        __syncthreads();
+        step(F{}, T{}, 0, kBK, kt0[half], vt0[half], kt1[half], vt1[half]);  // no DMA: tile 1 is loaded
+        tiles(T{}, F{}, T{}, kBK, kv_end);
+      } else {
+        const int c_end = min(kv_end, (kn0 + kBK - 1) / kBK * kBK);
+        tiles(F{}, T{}, F{}, 0, c_end);
+        tiles(T{}, F{}, F{}, c_end, kv_end);
+      }
+    } else {
+      tiles(F{}, T{}, F{}, 0, kv_end);
+    }
   } else {
     if (kv_end > 0) {
       fetch_bids(0);
@@ -916,8 +1008,14 @@ __device__ __forceinline__ void store_rows(const PrefillArgs& p, int wid) {
   }
 }
 
+// Waves per SIMD the registers must allow: two 4-wave workgroups per CU (their 64 KB of LDS each fits twice), two
+// 8-wave ones (at most 128 VGPRs: the riding store's paged form would take 132 and hold one workgroup per CU, which
+// ran the 44 x 46-token step's 264 workgroups in two rounds, 15.4 -> 17.6 us), one int8 workgroup (128 KB of LDS).
+constexpr int prefill_waves_per_simd(bool quant, int nw) { return quant ? 1 : (nw == 8 ? 4 : 2); }
+
 template <bool QUANT, int KV, int NW, int RT, int FORM>
-__global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 : 2) void prefill_kernel(PrefillArgs p) {
+__global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), prefill_waves_per_simd(QUANT, NW)) void prefill_kernel(
+    PrefillArgs p) {
   constexpr int NH = QUANT ? 2 : 1;
   __shared__ __attribute__((aligned(1024))) uint8_t kt0[NH][kTB];
   __shared__ __attribute__((aligned(1024))) uint8_t kt1[NH][kTB];
@@ -929,7 +1027,7 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
     const int n = p.batch * nz, id = blockIdx.x, r = id / n, c = (id + r) % n;
     const int qt = p.causal ? (int)gridDim.x / n - 1 - r : r;
     prefill_tile<QUANT, KV, NW, RT>(p, qt, c / nz, c % nz, bufs);
-    if constexpr (KV == kPacked || (KV == kPagedTilesRows && !QUANT))
+    if constexpr (KV == kPacked || KV == kPagedTilesRows)
       if (p.store_rows > 0 && id >= p.store_first && id < p.store_first + p.store_wgs) store_rows(p, id - p.store_first);
   } else if constexpr (FORM == kFormPersistent) {
     constexpr int NWV = NW * (QUANT ? 2 : 1);
@@ -949,7 +1047,7 @@ __global__ __launch_bounds__(64 * NW * (QUANT ? 2 : 1), (QUANT || NW == 8) ? 1 :
       if (p.causal) qt = (int)gridDim.x - 1 - qt;  // heavy query tiles first
     }
     prefill_tile<QUANT, KV, NW, RT>(p, qt, b, gz, bufs);
-    if constexpr (KV == kPacked || (KV == kPagedTilesRows && !QUANT)) {
+    if constexpr (KV == kPacked || KV == kPagedTilesRows) {
       if (p.store_rows > 0) {
         const int id = (int)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
         if (id >= p.store_first && id < p.store_first + p.store_wgs) store_rows(p, id - p.store_first);
@@ -1010,7 +1108,7 @@ hipError_t launch_prefill_kind(const PrefillArgs& a, dim3 grid, hipStream_t stre
   if (!a.block_tables)
     prefill_kernel<QUANT, kPacked, NW, RT, FORM><<<grid, block, 0, stream>>>(a);
   else if (a.block_size % kBK == 0 && a.new_from_rows) {
-    if constexpr (!QUANT && FORM != kFormPersistent)  // (the plain and rank-major bf16 forms take a riding store)
+    if constexpr (FORM != kFormPersistent)  // (the plain and rank-major forms take a riding store)
       prefill_kernel<QUANT, kPagedTilesRows, NW, RT, FORM><<<grid, block, 0, stream>>>(a);
     else
       return hipErrorInvalidValue;
@@ -1145,9 +1243,12 @@ hipError_t launch_prefill_int8(const PrefillArgs& a0, int max_seqlen_q, hipStrea
   PrefillArgs a = a0;
   a.xcd_order = (int64_t)q_tiles * a.batch >= kXcdOrderMinWorkgroups;
   const dim3 grid((unsigned)q_tiles, (unsigned)a.batch, 1u);
-  // a riding KV store (packed keys only) is copied by the launch's last min(grid, 256) workgroups after their items
+  // a riding KV store (packed keys, or paged tiles with the new keys from the rows) is copied by the launch's last
+  // min(grid, 256) workgroups after their items
+  if (a.new_from_rows && (!a.block_tables || a.block_size % kBK || !a.k_src || !a.v_src || a.store_rows <= 0))
+    return hipErrorInvalidValue;
   if (a.store_rows > 0) {
-    if (a.block_tables || !a.store_slots) return hipErrorInvalidValue;
+    if ((a.block_tables && !a.new_from_rows) || !a.store_slots) return hipErrorInvalidValue;
     const int64_t nwg = (int64_t)q_tiles * a.batch;
     a.store_wgs = (int)(nwg < 256 ? nwg : 256);
     a.store_first = (int)(nwg - a.store_wgs);

@@ -352,10 +352,10 @@ def prefill_attention_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k
     sequence's new keys from the rows and its merge kernel writes the caches; that needs slot_mapping to hold the
     slots the table gives the new tokens' positions, as the engine's does. Same outputs and caches as the two calls.
     ``plan``: as varlen_attention's (keys of its own, apart from varlen_attention's). ``quant``: the int8 output of
-    varlen_attention(quant=True), (int8 o [T, H * D], fp32 scale [T]); without a block table the copy rides in that
-    launch (vox_prefill_attn_int8_store, the W8A8 layer's short-prefill pair store_kvcache + short_causal_attention,
-    nanovllm_voxcpm/kernels/fused_layer.py:643-667), with one the two calls run. Reference: the prefill branch of
-    nanovllm_voxcpm/model/layers.py:326-348."""
+    varlen_attention(quant=True), (int8 o [T, H * D], fp32 scale [T]), with the copy riding in that launch
+    (vox_prefill_attn_int8_store: the W8A8 layer's store_kvcache + short_causal_attention pair without a block table,
+    its store_kvcache + paged_prefill_attention pair with one, nanovllm_voxcpm/kernels/fused_layer.py:619-667).
+    Reference: the prefill branch of nanovllm_voxcpm/model/layers.py:326-348."""
     T, H, D = q.shape
     N, HK, Dk = k.shape
     _require(k.stride(-1) == 1 and v.stride(-1) == 1, "key/value: last dim must be contiguous")
@@ -380,13 +380,19 @@ def prefill_attention_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k
     cu_k = _as_i32(cu_seqlens_k, "cu_seqlens_k")
     slots = _as_i32(slot_mapping.reshape(-1), "slot_mapping")
     lib = _lib.load()
+    bt = None
+    if block_table is not None:
+        _check_cuda(q, block_table)
+        if k_cache.dim() != 4 or k_cache.shape[2] != HK:
+            raise ValueError("with a block table the caches must be [num_blocks, block_size, HK, head_dim]")
+        bt = block_table if (block_table.dtype == torch.int32 and block_table.stride(1) == 1) else \
+            _as_i32(block_table, "block_table")
+        if bt.dim() != 2 or bt.shape[0] < B:
+            raise ValueError("block_table must be [B, max_blocks]")
+    # the cache as [num_blocks, block_size] slots (a flat [slots, HK, D] cache: one slot per block)
+    num_blocks, block_size = (k_cache.shape[0], k_cache.shape[1]) if k_cache.dim() == 4 else \
+        (k_cache.numel() // (HK * Dk), 1)
     if quant:
-        if block_table is not None:  # the paged int8 form: the store, then the attention over the caches
-            store_kvcache(k, v, k_cache, v_cache, slot_mapping)
-            return varlen_attention(q, None, None, cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_seqlens_k,
-                                    max_seqlen_q=max_seqlen_q, softmax_scale=softmax_scale, causal=causal,
-                                    block_table=block_table, k_cache=k_cache, v_cache=v_cache, quant=True,
-                                    inv_smooth=inv_smooth)
         out_q = torch.empty(T, H * D, dtype=torch.int8, device=dev)
         out_scale = torch.empty(T, dtype=torch.float32, device=dev)
         if inv_smooth is not None:
@@ -397,8 +403,9 @@ def prefill_attention_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k
         ws_bytes = lib.vox_prefill_int8_workspace_bytes(T, max(B, 0), int(max_seqlen_q), H, HK, D, 1 if causal else 0)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
         _lib.check(lib.vox_prefill_attn_int8_store(
-            q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(), k.stride(0), v.stride(0), slots.data_ptr(),
-            k_cache.data_ptr(), v_cache.data_ptr(), k_cache.numel() // (HK * Dk), N, cu_q.data_ptr(), cu_k.data_ptr(),
+            q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(), k.stride(0), v.stride(0), slots.data_ptr(), N,
+            k_cache.data_ptr(), v_cache.data_ptr(), num_blocks, block_size, None if bt is None else bt.data_ptr(),
+            0 if bt is None else bt.stride(0), 0 if bt is None else bt.shape[1], cu_q.data_ptr(), cu_k.data_ptr(),
             max(B, 0), int(max_seqlen_q) if T else 0, H, HK, D, float(softmax_scale), 1 if causal else 0,
             None if inv_smooth is None else inv_smooth.data_ptr(), out_q.data_ptr(), out_q.stride(0),
             out_scale.data_ptr(), T, None if ws is None else ws.data_ptr(), ws_bytes, _lib.stream_handle(dev)),
@@ -406,15 +413,7 @@ def prefill_attention_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k
         return out_q, out_scale
     if out is None:
         out = torch.empty(T, H, D, dtype=q.dtype, device=dev)
-    if block_table is not None:
-        _check_cuda(q, block_table)
-        if k_cache.dim() != 4 or k_cache.shape[2] != HK:
-            raise ValueError("with a block table the caches must be [num_blocks, block_size, HK, head_dim]")
-        num_blocks, block_size = k_cache.shape[0], k_cache.shape[1]
-        bt = block_table if (block_table.dtype == torch.int32 and block_table.stride(1) == 1) else \
-            _as_i32(block_table, "block_table")
-        if bt.dim() != 2 or bt.shape[0] < B:
-            raise ValueError("block_table must be [B, max_blocks]")
+    if bt is not None:
         # the mixed launch (and with it the riding store) where varlen_attention would run the one-query rows on the
         # decode kernels
         ws, mode = None, _lib.PLAN_NONE
