@@ -670,7 +670,8 @@ def _step_with_new_rows(gen, pre, prefix, dec, hk, block_size, misalign=0):
 
 
 @pytest.mark.parametrize("case", ["config5", "prefixes", "one_kv_head", "unaligned_rows", "planned", "dense",
-                                  "dense_8_waves", "dense_128_rows", "blocks_of_32"])
+                                  "dense_8_waves", "dense_128_rows", "dense_blocks_of_512", "blocks_of_128",
+                                  "blocks_of_32"])
 def test_paged_prefill_with_the_store_riding_in_it_equals_store_then_prefill(case):
     """prefill_attention_store with a block table (the launch reads each sequence's new keys from the rows and
     writes the caches) against store_kvcache then flash_attn_varlen_func over the caches: outputs and both caches
@@ -681,7 +682,7 @@ def test_paged_prefill_with_the_store_riding_in_it_equals_store_then_prefill(cas
     decode rows; one kv head; the config 5 step over three layers with a plan (record, reuse, reuse). Key / value rows
     that are not 16-byte aligned take the two calls. Dense prefills (no decode rows; the prefill launch's last
     workgroups write the caches), with cached prefixes: the rank-major 64-row form, the 8-wave form and the 128-row
-    form. 32-token blocks take the two calls."""
+    form; 512-token blocks (dense) and 128-token blocks (with decode rows). 32-token blocks take the two calls."""
     from voxcpm2_arabic_dialects_turbo_amd.ops import prefill_attention_store
 
     gen = torch.Generator().manual_seed(97)
@@ -698,6 +699,11 @@ def test_paged_prefill_with_the_store_riding_in_it_equals_store_then_prefill(cas
         pre, prefix, dec, bs = uniform_lens(gen, 3, 2400, 2600), [0, 45, 300], [], BLOCK
     elif case == "dense_128_rows":  # 6 x ~5600 tokens: 128-row items, more than 2048 workgroups
         pre, prefix, dec, bs = uniform_lens(gen, 6, 5500, 5700), [0, 1, 64, 250, 256, 700], [], 64
+    elif case == "dense_blocks_of_512":  # prefixes inside, at and past a block's first tile and its end
+        pre, prefix, dec, bs = uniform_lens(gen, 6, 50, 300), [0, 7, 100, 511, 512, 700], [], 512
+    elif case == "blocks_of_128":
+        pre, prefix, bs = uniform_lens(gen, 6, 20, 250), [0, 13, 127, 128, 200, 333], 128
+        dec = uniform_lens(gen, 40, 1, 900)
     else:  # blocks_of_32
         pre, prefix, dec, bs = uniform_lens(gen, 5, 50, 300), [0, 7, 40, 64, 90], uniform_lens(gen, 20, 1, 300), 32
     nq, nk, kc, vc, tables, q, k, v, slots = _step_with_new_rows(gen, pre, prefix, dec, hk, bs,
