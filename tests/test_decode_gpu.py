@@ -72,6 +72,18 @@ def test_decode_one_kv_head_tp2_shape():
     _check(randn(gen, 12, 8, D), kc, vc, lens, tables, "HK=1")
 
 
+@pytest.mark.parametrize("h,hk", [(1, 1), (2, 2), (4, 2), (6, 2), (10, 2), (13, 1), (16, 1)])
+def test_decode_every_group_size(h, hk):
+    """Any num_heads <= 16 over 1 or 2 kv heads (the ABI's contract): groups 1, 2, 3, 5, 13 and 16 besides the
+    model's 8. Heads past num_heads pad the 16 query columns of the MFMA tiles and must neither leak into the real
+    heads nor be written; contexts from 0 to beyond one workgroup's range (sequences cut by range boundaries)."""
+    gen = torch.Generator().manual_seed(70 + 3 * h + hk)
+    lens = [0, 1, 17, 256, 700] + uniform_lens(gen, 20, 1, 3000)
+    kc, vc, tables = paged_pool(gen, [max(n, 1) for n in lens], 400, hk=hk)
+    (_, _), out = _check(randn(gen, len(lens), h, D), kc, vc, lens, tables, f"{h}/{hk} heads", h=h, hk=hk)
+    assert out.shape == (len(lens), h, D) and int(out[0].abs().sum()) == 0
+
+
 def test_decode_strided_query_rows_and_small_blocks():
     """q as a view of the qkv output (rows 2560 elements apart); 64-token blocks."""
     gen = torch.Generator().manual_seed(34)
