@@ -169,8 +169,10 @@ def test_paged_block_sizes(bs):
     attn_close(out, want, f"paged block_size {bs}")
 
 
-@pytest.mark.parametrize("h,hk", [(16, 1), (8, 1), (16, 4), (4, 4)])
+@pytest.mark.parametrize("h,hk", [(16, 1), (8, 1), (16, 4), (4, 4), (16, 8), (64, 2), (64, 1), (128, 1)])
 def test_group_sizes(h, hk):
+    """Every group size that divides a workgroup's 128 rows: 1 to 16 query heads per kv head, and 32, 64 and 128,
+    where a 16-row wave holds part of one token's heads and an item fewer tokens than waves (128: one token)."""
     gen = torch.Generator().manual_seed(54 + h + hk)
     lens = [1, 70, 129, 33]
     T = sum(lens)
