@@ -329,6 +329,22 @@ def test_int8_two_pass_codes_equal_the_quantized_bf16_output(h, hk, smooth):
     assert torch.equal(codes.cpu(), q_ref), "codes differ from the quantized bf16 output's"
 
 
+@pytest.mark.parametrize("h,hk", [(4, 2), (8, 2), (2, 1), (32, 1), (64, 2), (64, 1), (128, 1)])
+def test_int8_group_sizes(h, hk):
+    """The int8 epilogue over group sizes 2, 4, 32, 64 and 128 (the model's 8 and 16 are covered above): one scale
+    per token over all h heads, where a 16-row wave may hold part of one token's heads (groups above 16) and the
+    token rows span both kv halves of the workgroup (hk = 2). Rows of more than 16 heads take the fused epilogue."""
+    gen = torch.Generator().manual_seed(95 + h + hk)
+    lens = [1, 70, 129, 33]
+    T = sum(lens)
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32)
+    q, k, v = (randn(gen, T, n, D) for n in (h, hk, hk))
+    out = varlen_attention(q.to(DEV), k.to(DEV), v.to(DEV), quant=True, cu_seqlens_q=cu.to(DEV),
+                           cu_seqlens_k=cu.to(DEV), max_seqlen_q=max(lens), softmax_scale=SCALE, causal=True)
+    torch.cuda.synchronize()
+    _check(out, ref.varlen(q.float(), cu, cu, k=k, v=v), f"int8 H={h} HK={hk}")
+
+
 def test_int8_two_pass_in_a_hip_graph_replays_like_eager():
     """The two-pass int8 form captured in a HIP graph (its workspace allocated inside the capture) and replayed four
     times, with eager calls on other inputs between the replays: every replay equals the eager result bit for bit."""
