@@ -566,6 +566,21 @@ def test_mixed_launch_with_many_decode_rows_per_workgroup(grid, h, hk):
         assert out[r].float().abs().max().item() == 0.0, "a one-query row without keys gives zeros"
 
 
+@pytest.mark.parametrize("h,hk", [(2, 2), (4, 2), (8, 2), (2, 1), (4, 1)])
+def test_mixed_launch_group_sizes(h, hk):
+    """The mixed launch at group sizes 1, 2 and 4 (the decode role's block-diagonal query columns mostly padding):
+    40 one-query rows over up to 1500 keys (sequences cut across decode workgroups, merged by the merge kernel) beside
+    5 prefills with cached prefixes, at the default decode grid."""
+    gen = torch.Generator().manual_seed(96 + 3 * h + hk)
+    nq, nk, kc, vc, tables = _mixed_case(gen, 40, 1500, uniform_lens(gen, 5, 2, 300), hk, block_size=BLOCK)
+    q = randn(gen, sum(nq), h, D)
+    out = flash_attn_varlen_func(q.to(DEV), kc.to(DEV), vc.to(DEV), _cu(nq).to(DEV), _cu(nk).to(DEV), max(nq),
+                                 max(nk), softmax_scale=SCALE, causal=True, block_table=tables.to(DEV))
+    torch.cuda.synchronize()
+    want = ref.varlen(q.float(), _cu(nq), _cu(nk), k_cache=kc, v_cache=vc, block_tables=tables)
+    attn_close(out, want, f"mixed launch, {h}/{hk} heads")
+
+
 @pytest.mark.parametrize("n_seq", [256, 257])
 def test_mixed_step_at_and_past_the_mixed_launch_limit(n_seq):
     """256 sequences run as one mixed launch, 257 as the persistent prefill launch then the decode launch: both
