@@ -84,6 +84,16 @@ def test_decode_every_group_size(h, hk):
     assert out.shape == (len(lens), h, D) and int(out[0].abs().sum()) == 0
 
 
+@pytest.mark.parametrize("bs", [96, 128, 512, 1024])
+def test_decode_block_sizes(bs):
+    """Block sizes the ABI accepts beside 32, 64 and 256 (any multiple of 32; 96 is not a power of two, so 16-token
+    steps start at every offset of a block): contexts around block boundaries and beyond one workgroup's range."""
+    gen = torch.Generator().manual_seed(80 + bs)
+    lens = [1, bs - 1, bs, bs + 1, 2 * bs + 17] + uniform_lens(gen, 16, 1, 4000)
+    kc, vc, tables = paged_pool(gen, lens, sum(-(-n // bs) for n in lens) + 3, block_size=bs)
+    _check(randn(gen, len(lens), H, D), kc, vc, lens, tables, f"block size {bs}")
+
+
 def test_decode_strided_query_rows_and_small_blocks():
     """q as a view of the qkv output (rows 2560 elements apart); 64-token blocks."""
     gen = torch.Generator().manual_seed(34)
