@@ -97,7 +97,8 @@ struct Tile {
 // Issues the loads of the 16-token tile whose first token sits at cache slot slot0 (a tile never straddles a cache
 // block). Every load is unconditional and in bounds, so the compiler can count outstanding loads exactly: the caller
 // maps an unmapped block to block 0 and masks what it read. K rows land in MFMA A layout (lane = token r16), V
-// pieces coalesced (16 bytes per lane, whole slot rows per instruction). slot0 is wave-uniform: each load is a
+// pieces coalesced (16 bytes per lane, whole slot rows per instruction; streaming loads, as every tile is read once
+// per launch). slot0 is wave-uniform: each load is a
 // uniform base plus a per-lane 32-bit byte offset that is the same for every tile (koff, voff) plus an immediate.
 template <int HK>
 __device__ __forceinline__ void load_tile(Tile<HK>& T, const DecodeArgs& p, int64_t slot0, uint32_t koff,
@@ -106,10 +107,10 @@ __device__ __forceinline__ void load_tile(Tile<HK>& T, const DecodeArgs& p, int6
   const char* kb = reinterpret_cast<const char*>(p.k_cache + slot0 * TT::ROW) + koff;
   const char* vb = reinterpret_cast<const char*>(p.v_cache + slot0 * TT::ROW) + voff;
 #pragma unroll
-  for (int kc = 0; kc < TT::KC; ++kc) T.k[kc] = ld_g16(kb + kc * 64);
+  for (int kc = 0; kc < TT::KC; ++kc) T.k[kc] = ld_g16_stream(kb + kc * 64);
   // V piece i covers 64 / PPR slot rows starting at row i * 64 / PPR: i * 1024 bytes past piece 0 for any HK
 #pragma unroll
-  for (int i = 0; i < TT::VP; ++i) T.v[i] = ld_g16(vb + i * 1024);
+  for (int i = 0; i < TT::VP; ++i) T.v[i] = ld_g16_stream(vb + i * 1024);
 }
 
 // load_tile in store mode: tile row r_new (-1: none) is the step's new token, read from its K / V rows nk / nv
@@ -124,13 +125,13 @@ __device__ __forceinline__ void load_tile_new(Tile<HK>& T, const DecodeArgs& p, 
   // K: lane (row r16, dims jq * 8 + ...): the new row's same dims, at koff less the row offset
   if ((lane & 15) == r_new) kb = reinterpret_cast<const char*>(nk) + (koff - (uint32_t)(r_new * TT::ROW) * 2u);
 #pragma unroll
-  for (int kc = 0; kc < TT::KC; ++kc) T.k[kc] = ld_g16(kb + kc * 64);
+  for (int kc = 0; kc < TT::KC; ++kc) T.k[kc] = ld_g16_stream(kb + kc * 64);
   // V piece i holds slot row i * 64 / PPR + lane / PPR, dims (lane % PPR) * 8
   const char* nvb = reinterpret_cast<const char*>(nv) + (uint32_t)((lane % TT::PPR) * 8) * 2u;
 #pragma unroll
   for (int i = 0; i < TT::VP; ++i) {
     const bool mine = i * (64 / TT::PPR) + lane / TT::PPR == r_new;
-    T.v[i] = ld_g16(mine ? nvb : vb + i * 1024);
+    T.v[i] = ld_g16_stream(mine ? nvb : vb + i * 1024);
   }
 }
 

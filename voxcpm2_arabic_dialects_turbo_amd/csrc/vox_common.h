@@ -32,6 +32,13 @@ __device__ __forceinline__ u32x4 zero4() { return u32x4{0u, 0u, 0u, 0u}; }
 // 16-byte global load (one dwordx4 per lane).
 __device__ __forceinline__ u32x4 ld_g16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 
+// The same load marked non-temporal (streaming): for data read once per launch, such as the decode kernel's KV cache
+// tiles, so that the stream does not evict from L2 what the launch reads again (its partials, plan records, block
+// tables, query rows). Measured on the 28-layer decode step of 150 sequences: 1.103 -> 1.045 ms.
+__device__ __forceinline__ u32x4 ld_g16_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
 // Round-to-nearest-even fp32 -> bf16 of two values packed low/high into one dword.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   typedef float f32x2 __attribute__((ext_vector_type(2)));
