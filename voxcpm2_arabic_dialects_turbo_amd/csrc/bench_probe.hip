@@ -7,9 +7,9 @@
 //  * tile_read_kernel: the decode kernel's access pattern without its arithmetic. A list of 16-token tiles (byte
 //    offsets of 16 contiguous 512-byte slot rows inside the K plane; the V tile sits at the same offset in the V
 //    plane) is cut into equal contiguous ranges, one per workgroup of 4 waves, each wave taking every fourth tile of
-//    its range. Per tile a wave issues the decode kernel's loads: K as 8 loads in MFMA A-operand layout (lane =
-//    token, 16 bytes at 64-byte steps), V as 8 coalesced loads (1 KiB per instruction). DEPTH tiles are in flight
-//    per wave (the decode kernel keeps one).
+//    its range. Per tile a wave issues the decode kernel's loads, streaming as there: K as 8 loads in MFMA A-operand
+//    layout (lane = token, 16 bytes at 64-byte steps), V as 8 coalesced loads (1 KiB per instruction). DEPTH tiles
+//    are in flight per wave (the decode kernel keeps one).
 // Every loaded word is folded into an XOR that is stored only if it hits an impossible value, so no load is dead.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -49,9 +49,9 @@ __global__ __launch_bounds__(kProbeThreads) void tile_read_kernel(const char* __
   auto issue = [&](int slot, int64_t t) {
     const int64_t off = tiles[t];
 #pragma unroll
-    for (int kc = 0; kc < 8; ++kc) kr[slot][kc] = ld_g16(kp + off + koff + kc * 64);
+    for (int kc = 0; kc < 8; ++kc) kr[slot][kc] = ld_g16_stream(kp + off + koff + kc * 64);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) vr[slot][i] = ld_g16(vp + off + voff + i * 1024);
+    for (int i = 0; i < 8; ++i) vr[slot][i] = ld_g16_stream(vp + off + voff + i * 1024);
   };
   int64_t t = lo + w;
 #pragma unroll
